@@ -1,0 +1,172 @@
+/*
+ * rmoe.h - C ABI of the MI355X-native quantized sparse-MoE block.
+ *
+ * All tensor pointers are caller-owned DEVICE pointers (for instance the
+ * data_ptr() of torch tensors on the GPU); every compute call is enqueued on
+ * `stream` (a hipStream_t passed as void*, NULL = the default stream) and
+ * returns without waiting for the GPU.  Every call returns RMOE_OK (0) or a
+ * negative RMOE_E* code; the message for the last failure on the calling
+ * thread is rmoe_last_error().  Arguments are validated on the host before
+ * anything is launched, so argument errors never reach the GPU.  No call
+ * allocates device memory: scratch space is the caller's `workspace`,
+ * which must be zero-filled once when it is first allocated (the library
+ * keeps its counters at a fixed offset and leaves them at zero when each
+ * call completes, so one workspace serves calls of any shape) and must not
+ * be shared by calls that may run concurrently.
+ *
+ * Weight format (MLX "affine", transpose=True): a matrix W[out, in] of
+ * `bits`-bit codes is stored as uint32 words [out, in * bits / 32], element
+ * k of a row in word k / (32/bits) at bit offset bits * (k % (32/bits)),
+ * least-significant first; scales and biases are bf16 [out, in / group];
+ * W[r, k] = q * scale + bias.  Expert banks add a leading [experts] axis.
+ * bf16 values travel as uint16_t bit patterns.
+ *
+ * Reference interfaces replaced (paths relative to the waylake/runnel tree):
+ *   rmoe_switch_glu   FusedQuantizedSwitchGLU.__call__   src/runnel/mlx.py:57-82
+ *   rmoe_gather_qmm   mx.gather_qmm / QuantizedSwitchLinear, called at
+ *                     src/runnel/mlx.py:64-75 and :77-79
+ *   rmoe_moe_block    mlx-lm SparseMoeBlock.__call__ (the caller of the
+ *                     module, invoked as layer.mlp(x) at
+ *                     bench/mlx_component_profile.py:130)
+ *   rmoe_router       the router half of that block (gate -> softmax ->
+ *                     top-k -> renormalise)
+ *   rmoe_quantize / rmoe_dequantize
+ *                     mx.quantize / mx.dequantize (affine, group 64), the
+ *                     format produced for the banks that
+ *                     src/runnel/mlx.py:38-48 concatenates
+ *   rmoe_stream_read  the HBM stream calibrator that replaces
+ *                     native/shaders/persistent_stream.metal:12-79
+ */
+#ifndef RMOE_H
+#define RMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RMOE_ABI_VERSION 1
+
+#define RMOE_OK 0
+#define RMOE_EINVAL (-1) /* inconsistent or unsupported shape / argument */
+#define RMOE_EBITS (-2)  /* bits not in {4, 8} or group size not 64 */
+#define RMOE_EALIGN (-3) /* a pointer is not 16-byte aligned */
+#define RMOE_EWS (-4)    /* workspace missing or too small */
+#define RMOE_EHIP (-5)   /* the HIP runtime reported an error */
+#define RMOE_ENULL (-6)  /* a required pointer is NULL */
+
+/* One MLX-affine quantized bank: w [experts, rows, cols*bits/32] u32,
+ * scales / biases [experts, rows, cols/group_size] bf16. */
+typedef struct rmoe_qweight {
+  const uint32_t* w;
+  const uint16_t* scales;
+  const uint16_t* biases;
+  int32_t experts;
+  int32_t rows;
+  int32_t cols;
+  int32_t bits;
+  int32_t group_size;
+} rmoe_qweight;
+
+/* One MoE layer's resident weights.  gate_up rows are [up; gate]
+ * (src/runnel/mlx.py:38-48).  The shared expert is present when
+ * shared_gate_up.w != NULL; shared_gate_w (bf16 [hidden]) is its sigmoid
+ * gate.  norm_topk_prob != 0 renormalises the selected probabilities. */
+typedef struct rmoe_layer {
+  int32_t hidden;
+  int32_t inter;
+  int32_t shared_inter;
+  int32_t experts;
+  int32_t top_k;
+  int32_t norm_topk_prob;
+  const uint16_t* router_w;      /* bf16 [experts, hidden] */
+  const uint16_t* shared_gate_w; /* bf16 [hidden], or NULL */
+  rmoe_qweight gate_up;          /* [experts, 2*inter, hidden] */
+  rmoe_qweight down;             /* [experts, hidden, inter] */
+  rmoe_qweight shared_gate_up;   /* [1, 2*shared_inter, hidden] */
+  rmoe_qweight shared_down;      /* [1, hidden, shared_inter] */
+} rmoe_layer;
+
+int rmoe_abi_version(void);
+const char* rmoe_last_error(void);
+const char* rmoe_status_string(int status);
+
+/* Host-only validation of a layer description (no GPU access). */
+int rmoe_validate_layer(const rmoe_layer* layer);
+
+/* Bytes of workspace the block / router / switch calls need for `tokens`. */
+size_t rmoe_workspace_bytes(const rmoe_layer* layer, int32_t tokens);
+
+/* Router of mlx-lm's SparseMoeBlock: bf16 logits x . router_w^T (fixed fp32
+ * reduction order), top_k experts by (logit desc, index asc), softmax over
+ * all experts, probabilities rounded to bf16, renormalised when
+ * norm_topk_prob.  indices int32 [tokens, top_k] in rank order, scores
+ * fp32 [tokens, top_k] (bf16-valued). */
+int rmoe_router(const uint16_t* router_w, int32_t experts, int32_t hidden,
+                int32_t top_k, int32_t norm_topk_prob, const uint16_t* x,
+                int32_t tokens, int32_t* indices, float* scores,
+                void* workspace, size_t workspace_bytes, void* stream);
+size_t rmoe_router_workspace_bytes(int32_t experts, int32_t top_k,
+                                   int32_t tokens);
+
+/* FusedQuantizedSwitchGLU.__call__ (src/runnel/mlx.py:57-82): for every
+ * (token, slot) the packed [up; gate] projection of expert indices[t, j],
+ * SwiGLU, then the expert's down projection.  y bf16 [tokens, top_k,
+ * hidden], per slot and not combined.  A slot whose index is outside
+ * [0, experts) yields a zero row and touches no weight memory. */
+int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
+                    const uint16_t* x, int32_t tokens, const int32_t* indices,
+                    int32_t top_k, uint16_t* y, void* workspace,
+                    size_t workspace_bytes, void* stream);
+size_t rmoe_switch_workspace_bytes(const rmoe_qweight* gate_up,
+                                   const rmoe_qweight* down, int32_t tokens,
+                                   int32_t top_k);
+
+/* gather_qmm(x, w, scales, biases, rhs_indices, transpose=True):
+ * y[m] = x[lhs[m]] . deq(w[rhs[m]])^T for m < rows.  lhs_indices == NULL
+ * means row m reads x[m]; rhs_indices == NULL means expert 0; a row whose
+ * index is out of range is written as zeros.  x bf16 [x_rows, w->cols];
+ * exactly one of y_bf16 / y_f32 ([rows, w->rows]) is non-NULL. */
+int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows,
+                    const int32_t* lhs_indices, const int32_t* rhs_indices,
+                    int32_t rows, const rmoe_qweight* w, uint16_t* y_bf16,
+                    float* y_f32, void* stream);
+
+/* Whole block (mlx-lm SparseMoeBlock.__call__): out[t] = bf16(sum_j
+ * score_j * y_j + bf16(sigmoid(x . shared_gate_w)) * y_shared); with
+ * residual != NULL, out[t] = bf16(residual[t] + out[t]).  indices_out /
+ * scores_out may be NULL.  x, residual, out bf16 [tokens, hidden]; out may
+ * alias residual but not x. */
+int rmoe_moe_block(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
+                   const uint16_t* residual, uint16_t* out,
+                   int32_t* indices_out, float* scores_out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Affine quantization of fp32 rows [rows, cols] (group_size 64, bits 4|8):
+ * per group, the larger-magnitude edge value is kept exact, scale and bias
+ * are rounded to bf16 and the codes are round-half-even((w - b) / s)
+ * clipped to [0, 2^bits - 1]. */
+int rmoe_quantize(const float* w, int64_t rows, int32_t cols, int32_t bits,
+                  int32_t group_size, uint32_t* wq, uint16_t* scales,
+                  uint16_t* biases, void* stream);
+
+/* Dequantize rows [row_begin, row_begin + rows) of the flattened bank
+ * (experts * rows) to fp32 fl32(q*s + b) (out_f32) and/or to bf16 of that
+ * value (out_bf16); either output may be NULL. */
+int rmoe_dequantize(const rmoe_qweight* w, int64_t row_begin, int64_t rows,
+                    float* out_f32, uint16_t* out_bf16, void* stream);
+
+/* Reads `bytes` (a multiple of 16) once with 16-byte loads using `blocks`
+ * workgroups of 256 lanes; workgroup i folds what it read into partials[i]
+ * (device uint32 [blocks], overwritten).  Measures achievable HBM read
+ * bandwidth for a given launch shape. */
+int rmoe_stream_read(const void* buffer, size_t bytes, uint32_t* partials,
+                     int32_t blocks, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RMOE_H */

@@ -1,0 +1,440 @@
+// C ABI: host-side validation and dispatch.  Every argument is checked
+// before anything is launched; failures return a negative RMOE_E* code and
+// leave a message for rmoe_last_error().  Nothing here allocates device
+// memory.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "kernels.h"
+#include "rmoe.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return RMOE_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(RMOE_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int values_per_chunk(int bits) { return bits == 8 ? 16 : 32; }
+
+int check_qweight(const rmoe_qweight* q, const char* name) {
+  if (!q) return fail(RMOE_ENULL, "%s: descriptor is NULL", name);
+  if (!q->w || !q->scales || !q->biases)
+    return fail(RMOE_ENULL, "%s: weight, scales and biases are required", name);
+  if (q->bits != 4 && q->bits != 8)
+    return fail(RMOE_EBITS, "%s: bits must be 4 or 8 (got %d)", name, q->bits);
+  if (q->group_size != 64)
+    return fail(RMOE_EBITS, "%s: group_size must be 64 (got %d)", name,
+                q->group_size);
+  if (q->experts < 1 || q->rows < 1 || q->cols < 64 || q->cols % 64)
+    return fail(RMOE_EINVAL,
+                "%s: need experts >= 1, rows >= 1, cols a positive multiple of "
+                "64 (got %d, %d, %d)",
+                name, q->experts, q->rows, q->cols);
+  if (!aligned(q->w, 16))
+    return fail(RMOE_EALIGN, "%s: packed weight must be 16-byte aligned", name);
+  if (!aligned(q->scales, 2) || !aligned(q->biases, 2))
+    return fail(RMOE_EALIGN, "%s: scales/biases must be 2-byte aligned", name);
+  return RMOE_OK;
+}
+
+// The down-projection kernel maps one row onto inter/values_per_chunk lanes.
+int check_down_width(int inter, int bits, const char* name) {
+  const int chunks = inter / values_per_chunk(bits);
+  if (inter % values_per_chunk(bits) || !pow2(chunks) || chunks > 64)
+    return fail(RMOE_EINVAL,
+                "%s: intermediate size %d unsupported at %d bits (needs "
+                "inter/%d a power of two <= 64)",
+                name, inter, bits, values_per_chunk(bits));
+  return RMOE_OK;
+}
+
+int check_layer(const rmoe_layer* L) {
+  if (!L) return fail(RMOE_ENULL, "layer is NULL");
+  if (L->hidden < 64 || L->hidden % 64)
+    return fail(RMOE_EINVAL, "hidden must be a positive multiple of 64 (got %d)",
+                L->hidden);
+  if (L->inter < 64 || L->inter % 64)
+    return fail(RMOE_EINVAL, "inter must be a positive multiple of 64 (got %d)",
+                L->inter);
+  if (L->experts < 1 || L->experts > rmoe::kMaxExperts)
+    return fail(RMOE_EINVAL, "experts must be in [1, %d] (got %d)",
+                rmoe::kMaxExperts, L->experts);
+  if (L->top_k < 1 || L->top_k > rmoe::kMaxTopK || L->top_k > L->experts)
+    return fail(RMOE_EINVAL, "top_k must be in [1, min(%d, experts)] (got %d)",
+                rmoe::kMaxTopK, L->top_k);
+  if (!L->router_w) return fail(RMOE_ENULL, "router_w is NULL");
+  if (!aligned(L->router_w, 16))
+    return fail(RMOE_EALIGN, "router_w must be 16-byte aligned");
+  int rc;
+  if ((rc = check_qweight(&L->gate_up, "gate_up"))) return rc;
+  if ((rc = check_qweight(&L->down, "down"))) return rc;
+  if (L->gate_up.experts != L->experts || L->gate_up.rows != 2 * L->inter ||
+      L->gate_up.cols != L->hidden)
+    return fail(RMOE_EINVAL, "gate_up must be [experts, 2*inter, hidden]");
+  if (L->down.experts != L->experts || L->down.rows != L->hidden ||
+      L->down.cols != L->inter)
+    return fail(RMOE_EINVAL, "down must be [experts, hidden, inter]");
+  if (L->gate_up.bits != L->down.bits)
+    return fail(RMOE_EBITS, "gate_up and down must share one bit width");
+  if ((rc = check_down_width(L->inter, L->down.bits, "down"))) return rc;
+  const bool has_shared = L->shared_gate_up.w != nullptr;
+  if (has_shared) {
+    if ((rc = check_qweight(&L->shared_gate_up, "shared_gate_up"))) return rc;
+    if ((rc = check_qweight(&L->shared_down, "shared_down"))) return rc;
+    if (L->shared_inter != L->inter)
+      return fail(RMOE_EINVAL,
+                  "shared_inter must equal inter (got %d vs %d)",
+                  L->shared_inter, L->inter);
+    if (L->shared_gate_up.experts != 1 ||
+        L->shared_gate_up.rows != 2 * L->shared_inter ||
+        L->shared_gate_up.cols != L->hidden)
+      return fail(RMOE_EINVAL, "shared_gate_up must be [1, 2*shared_inter, hidden]");
+    if (L->shared_down.experts != 1 || L->shared_down.rows != L->hidden ||
+        L->shared_down.cols != L->shared_inter)
+      return fail(RMOE_EINVAL, "shared_down must be [1, hidden, shared_inter]");
+    if (L->shared_gate_up.bits != L->gate_up.bits ||
+        L->shared_down.bits != L->gate_up.bits)
+      return fail(RMOE_EBITS, "shared expert must use the routed bit width");
+  } else if (L->shared_gate_w) {
+    return fail(RMOE_EINVAL, "shared_gate_w given without a shared expert");
+  }
+  if (L->shared_gate_w && !aligned(L->shared_gate_w, 16))
+    return fail(RMOE_EALIGN, "shared_gate_w must be 16-byte aligned");
+  return RMOE_OK;
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Workspace carve-up shared by the router, switch and block calls.
+struct Layout {
+  size_t logits, idx, scores, act, ctr, total;
+};
+
+// The per-token counters sit at a fixed offset with room for the largest
+// token count, so a workspace reused by calls of different shapes always
+// finds them at zero (every kernel leaves them at zero when it finishes).
+Layout layout(int T, int E, int K, int I) {
+  Layout l{};
+  size_t off = 0;
+  l.ctr = off;
+  off = align_up(off + (size_t)(rmoe::kMaxTokens + 1) * sizeof(uint32_t));
+  l.logits = off;
+  off = align_up(off + (size_t)T * (E + 1) * sizeof(float));
+  l.idx = off;
+  off = align_up(off + (size_t)T * K * sizeof(int32_t));
+  l.scores = off;
+  off = align_up(off + (size_t)T * (K + 1) * sizeof(float));
+  l.act = off;
+  off = align_up(off + (size_t)T * (K + 1) * I * sizeof(float));
+  l.total = off;
+  return l;
+}
+
+rmoe::QW qw(const rmoe_qweight& q) { return rmoe::QW{q.w, q.scales, q.biases}; }
+
+int check_tokens(int32_t tokens) {
+  if (tokens < 0 || tokens > rmoe::kMaxTokens)
+    return fail(RMOE_EINVAL, "tokens must be in [0, %d] (got %d)", rmoe::kMaxTokens, tokens);
+  return RMOE_OK;
+}
+
+int check_ws(void* ws, size_t have, size_t need) {
+  if (need == 0) return RMOE_OK;
+  if (!ws) return fail(RMOE_EWS, "workspace is NULL (%zu bytes needed)", need);
+  if (have < need)
+    return fail(RMOE_EWS, "workspace too small: %zu bytes given, %zu needed", have,
+                need);
+  if (!aligned(ws, 256)) return fail(RMOE_EALIGN, "workspace must be 256-byte aligned");
+  return RMOE_OK;
+}
+
+rmoe::DecodeArgs decode_args(const rmoe_layer* L, const uint16_t* x, int T,
+                             void* ws) {
+  const Layout l = layout(T, L->experts, L->top_k, L->inter);
+  char* base = static_cast<char*>(ws);
+  rmoe::DecodeArgs a{};
+  a.T = T;
+  a.H = L->hidden;
+  a.I = L->inter;
+  a.E = L->experts;
+  a.K = L->top_k;
+  a.has_shared = L->shared_gate_up.w != nullptr;
+  a.norm = L->norm_topk_prob != 0;
+  a.switch_mode = 0;
+  a.x = x;
+  a.router_w = L->router_w;
+  a.sgate_w = a.has_shared ? L->shared_gate_w : nullptr;
+  a.gu = qw(L->gate_up);
+  a.dn = qw(L->down);
+  a.sgu = qw(L->shared_gate_up);
+  a.sdn = qw(L->shared_down);
+  a.logits = reinterpret_cast<float*>(base + l.logits);
+  a.idx = reinterpret_cast<int32_t*>(base + l.idx);
+  a.scores = reinterpret_cast<float*>(base + l.scores);
+  a.act = reinterpret_cast<float*>(base + l.act);
+  a.ctr = reinterpret_cast<uint32_t*>(base + l.ctr);
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rmoe_abi_version(void) { return RMOE_ABI_VERSION; }
+
+const char* rmoe_last_error(void) { return g_error.c_str(); }
+
+const char* rmoe_status_string(int status) {
+  switch (status) {
+    case RMOE_OK: return "ok";
+    case RMOE_EINVAL: return "invalid argument";
+    case RMOE_EBITS: return "unsupported quantization format";
+    case RMOE_EALIGN: return "misaligned pointer";
+    case RMOE_EWS: return "workspace too small";
+    case RMOE_EHIP: return "HIP runtime error";
+    case RMOE_ENULL: return "NULL pointer";
+    default: return "unknown status";
+  }
+}
+
+int rmoe_validate_layer(const rmoe_layer* layer) {
+  const int rc = check_layer(layer);
+  return rc ? rc : ok();
+}
+
+size_t rmoe_workspace_bytes(const rmoe_layer* L, int32_t tokens) {
+  if (check_layer(L) || tokens < 0) return 0;
+  return layout(tokens, L->experts, L->top_k, L->inter).total;
+}
+
+size_t rmoe_switch_workspace_bytes(const rmoe_qweight* gate_up,
+                                   const rmoe_qweight* down, int32_t tokens,
+                                   int32_t top_k) {
+  if (!gate_up || !down || tokens < 0 || top_k < 1) return 0;
+  return layout(tokens, gate_up->experts, top_k, gate_up->rows / 2).total;
+}
+
+size_t rmoe_router_workspace_bytes(int32_t experts, int32_t top_k, int32_t tokens) {
+  if (experts < 1 || top_k < 1 || tokens < 0) return 0;
+  return layout(tokens, experts, top_k, 0).total;
+}
+
+int rmoe_router(const uint16_t* router_w, int32_t experts, int32_t hidden,
+                int32_t top_k, int32_t norm_topk_prob, const uint16_t* x,
+                int32_t tokens, int32_t* indices, float* scores, void* ws,
+                size_t ws_bytes, void* stream) {
+  int rc;
+  if (hidden < 64 || hidden % 64)
+    return fail(RMOE_EINVAL, "hidden must be a positive multiple of 64 (got %d)", hidden);
+  if (experts < 1 || experts > rmoe::kMaxExperts)
+    return fail(RMOE_EINVAL, "experts must be in [1, %d] (got %d)", rmoe::kMaxExperts,
+                experts);
+  if (top_k < 1 || top_k > rmoe::kMaxTopK || top_k > experts)
+    return fail(RMOE_EINVAL, "top_k must be in [1, min(%d, experts)] (got %d)",
+                rmoe::kMaxTopK, top_k);
+  if ((rc = check_tokens(tokens))) return rc;
+  if (!router_w) return fail(RMOE_ENULL, "router_w is NULL");
+  if (!aligned(router_w, 16)) return fail(RMOE_EALIGN, "router_w must be 16-byte aligned");
+  if (tokens == 0) return ok();
+  if (!x || !indices || !scores) return fail(RMOE_ENULL, "x, indices and scores are required");
+  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  const size_t need = layout(tokens, experts, top_k, 0).total;
+  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  rmoe_layer L{};
+  L.hidden = hidden;
+  L.inter = 0;
+  L.experts = experts;
+  L.top_k = top_k;
+  L.norm_topk_prob = norm_topk_prob;
+  L.router_w = router_w;
+  rmoe::DecodeArgs a = decode_args(&L, x, tokens, ws);
+  a.idx_out = indices;
+  a.scores_out = scores;
+  const hipError_t e = rmoe::launch_router(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  return ok();
+}
+
+int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
+                   const uint16_t* residual, uint16_t* out, int32_t* indices_out,
+                   float* scores_out, void* ws, size_t ws_bytes, void* stream) {
+  int rc;
+  if ((rc = check_layer(L))) return rc;
+  if ((rc = check_tokens(tokens))) return rc;
+  if (tokens == 0) return ok();
+  if (!x || !out) return fail(RMOE_ENULL, "x and out are required");
+  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  if (!aligned(out, 2) || (residual && !aligned(residual, 2)))
+    return fail(RMOE_EALIGN, "out/residual must be 2-byte aligned");
+  if (static_cast<const void*>(out) == static_cast<const void*>(x))
+    return fail(RMOE_EINVAL, "out must not alias x");
+  const size_t need = layout(tokens, L->experts, L->top_k, L->inter).total;
+  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  rmoe::DecodeArgs a = decode_args(L, x, tokens, ws);
+  a.out = out;
+  a.residual = residual;
+  a.idx_out = indices_out;
+  a.scores_out = scores_out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bits = L->gate_up.bits;
+  hipError_t e = rmoe::launch_router(a, s);
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  e = rmoe::launch_gate_up(a, bits, s);
+  if (e != hipSuccess) return hip_fail(e, "gate/up launch");
+  e = rmoe::launch_down(a, bits, true, s);
+  if (e != hipSuccess) return hip_fail(e, "down launch");
+  return ok();
+}
+
+int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
+                    const uint16_t* x, int32_t tokens, const int32_t* indices,
+                    int32_t top_k, uint16_t* y, void* ws, size_t ws_bytes,
+                    void* stream) {
+  int rc;
+  if ((rc = check_qweight(gate_up, "gate_up"))) return rc;
+  if ((rc = check_qweight(down, "down"))) return rc;
+  if ((rc = check_tokens(tokens))) return rc;
+  if (gate_up->rows % 2) return fail(RMOE_EINVAL, "gate_up rows must be 2*inter");
+  const int I = gate_up->rows / 2;
+  const int H = gate_up->cols;
+  if (down->experts != gate_up->experts || down->rows != H || down->cols != I)
+    return fail(RMOE_EINVAL, "down must be [experts, hidden, inter] of gate_up");
+  if (down->bits != gate_up->bits)
+    return fail(RMOE_EBITS, "gate_up and down must share one bit width");
+  if ((rc = check_down_width(I, down->bits, "down"))) return rc;
+  if (top_k < 1 || top_k > rmoe::kMaxTopK)
+    return fail(RMOE_EINVAL, "top_k must be in [1, %d] (got %d)", rmoe::kMaxTopK, top_k);
+  if (tokens == 0) return ok();
+  if (!x || !indices || !y) return fail(RMOE_ENULL, "x, indices and y are required");
+  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  if (!aligned(indices, 4) || !aligned(y, 2))
+    return fail(RMOE_EALIGN, "indices/y misaligned");
+  const size_t need = layout(tokens, gate_up->experts, top_k, I).total;
+  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  rmoe_layer L{};
+  L.hidden = H;
+  L.inter = I;
+  L.experts = gate_up->experts;
+  L.top_k = top_k;
+  L.gate_up = *gate_up;
+  L.down = *down;
+  rmoe::DecodeArgs a = decode_args(&L, x, tokens, ws);
+  a.idx = const_cast<int32_t*>(indices);
+  a.switch_mode = 1;
+  a.out = y;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = rmoe::launch_gate_up(a, gate_up->bits, s);
+  if (e != hipSuccess) return hip_fail(e, "gate/up launch");
+  e = rmoe::launch_down(a, gate_up->bits, false, s);
+  if (e != hipSuccess) return hip_fail(e, "down launch");
+  return ok();
+}
+
+int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows, const int32_t* lhs,
+                    const int32_t* rhs, int32_t rows, const rmoe_qweight* w,
+                    uint16_t* y_bf16, float* y_f32, void* stream) {
+  int rc;
+  if ((rc = check_qweight(w, "w"))) return rc;
+  if (rows < 0 || x_rows < 0) return fail(RMOE_EINVAL, "rows must be >= 0");
+  if ((y_bf16 == nullptr) == (y_f32 == nullptr))
+    return fail(RMOE_EINVAL, "exactly one of y_bf16 / y_f32 must be given");
+  const int vpc = values_per_chunk(w->bits);
+  const int chunks = w->cols / vpc;
+  if (chunks < 64 && !pow2(chunks))
+    return fail(RMOE_EINVAL, "cols %d unsupported at %d bits", w->cols, w->bits);
+  if (chunks > 256)
+    return fail(RMOE_EINVAL, "cols %d too large (max %d at %d bits)", w->cols,
+                256 * vpc, w->bits);
+  if (rows == 0) return ok();
+  if (!x) return fail(RMOE_ENULL, "x is required");
+  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  rmoe::QmvArgs a{};
+  a.M = rows;
+  a.N = w->rows;
+  a.K = w->cols;
+  a.x_rows = lhs ? x_rows : rows;
+  a.experts = w->experts;
+  a.x = x;
+  a.lhs = lhs;
+  a.rhs = rhs;
+  a.w = qw(*w);
+  a.y_bf16 = y_bf16;
+  a.y_f32 = y_f32;
+  const hipError_t e = rmoe::launch_qmv(a, w->bits, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "qmv launch");
+  return ok();
+}
+
+int rmoe_quantize(const float* w, int64_t rows, int32_t cols, int32_t bits,
+                  int32_t group_size, uint32_t* wq, uint16_t* scales,
+                  uint16_t* biases, void* stream) {
+  if (bits != 4 && bits != 8) return fail(RMOE_EBITS, "bits must be 4 or 8");
+  if (group_size != 64) return fail(RMOE_EBITS, "group_size must be 64");
+  if (rows < 0 || cols < 64 || cols % 64)
+    return fail(RMOE_EINVAL, "cols must be a positive multiple of 64");
+  if (rows == 0) return ok();
+  if (!w || !wq || !scales || !biases) return fail(RMOE_ENULL, "all buffers are required");
+  if (!aligned(w, 16) || !aligned(wq, 4))
+    return fail(RMOE_EALIGN, "w must be 16-byte aligned");
+  const hipError_t e = rmoe::launch_quantize(w, rows, cols, bits, wq, scales, biases,
+                                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  return ok();
+}
+
+int rmoe_dequantize(const rmoe_qweight* w, int64_t row_begin, int64_t rows,
+                    float* out_f32, uint16_t* out_bf16, void* stream) {
+  int rc;
+  if ((rc = check_qweight(w, "w"))) return rc;
+  const int64_t total = (int64_t)w->experts * w->rows;
+  if (row_begin < 0 || rows < 0 || row_begin + rows > total)
+    return fail(RMOE_EINVAL, "row range [%lld, %lld) outside the bank of %lld rows",
+                (long long)row_begin, (long long)(row_begin + rows), (long long)total);
+  if (rows == 0 || (!out_f32 && !out_bf16)) return ok();
+  const hipError_t e =
+      rmoe::launch_dequantize(qw(*w), w->cols, w->bits, row_begin, rows, out_f32,
+                              out_bf16, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+  return ok();
+}
+
+int rmoe_stream_read(const void* buffer, size_t bytes, uint32_t* partials,
+                     int32_t blocks, void* stream) {
+  if (!buffer || !partials) return fail(RMOE_ENULL, "buffer and partials are required");
+  if (bytes % 16 || !aligned(buffer, 16))
+    return fail(RMOE_EALIGN, "buffer must be 16-byte aligned and a multiple of 16 bytes");
+  if (blocks < 1 || blocks > (1 << 20))
+    return fail(RMOE_EINVAL, "blocks must be in [1, 2^20]");
+  const hipError_t e = rmoe::launch_stream_read(buffer, bytes, partials, blocks,
+                                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "stream launch");
+  return ok();
+}
+
+}  // extern "C"

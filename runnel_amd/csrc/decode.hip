@@ -1,0 +1,463 @@
+// Decode-shaped kernels of the MoE block for gfx950 (wave64).
+//
+//   router_kernel   one wave per router row (fixed-order bf16 dot), then the
+//                   last workgroup of each token ranks the logits with wave
+//                   ballots/maxima: top-k, softmax, renormalisation, shared
+//                   sigmoid gate.
+//   gate_up_kernel  one wave per (up row c, gate row c + I) pair of one
+//                   selected expert: 16-byte streaming loads, dequantised in
+//                   registers, SwiGLU in the epilogue.  The shared expert is
+//                   the (k+1)-th unit of every token.
+//   down_kernel     one wave per group of output rows, all units of a token:
+//                   the router-weighted combine and the gated shared expert
+//                   are summed in registers, bf16 written once.
+//   qmv_kernel      plain gather-QMV (mx.gather_qmm at M rows).
+#include "common.h"
+#include "kernels.h"
+
+namespace rmoe {
+
+// ------------------------------------------------------------------ router
+__global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
+  const int t = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int has_sg = p.sgate_w != nullptr;
+  const int R = p.E + has_sg;
+  const int row = blockIdx.x * 4 + wave;
+  const uint16_t* xt = p.x + (size_t)t * p.H;
+  float* lg = p.logits + (size_t)t * (p.E + 1);
+  if (row < R) {
+    const uint16_t* wr =
+        row < p.E ? p.router_w + (size_t)row * p.H : p.sgate_w;
+    float acc = 0.0f;
+    const int chunks = p.H >> 3;
+    for (int c = lane; c < chunks; c += 64) {
+      const uint4 xv = load16(xt + c * 8);
+      const uint4 wv = load16_stream(wr + c * 8);
+      acc = fmaf(bf16_lo(xv.x), bf16_lo(wv.x), acc);
+      acc = fmaf(bf16_hi(xv.x), bf16_hi(wv.x), acc);
+      acc = fmaf(bf16_lo(xv.y), bf16_lo(wv.y), acc);
+      acc = fmaf(bf16_hi(xv.y), bf16_hi(wv.y), acc);
+      acc = fmaf(bf16_lo(xv.z), bf16_lo(wv.z), acc);
+      acc = fmaf(bf16_hi(xv.z), bf16_hi(wv.z), acc);
+      acc = fmaf(bf16_lo(xv.w), bf16_lo(wv.w), acc);
+      acc = fmaf(bf16_hi(xv.w), bf16_hi(wv.w), acc);
+    }
+    acc = wave_sum_butterfly(acc);
+    if (lane == 0) lg[row] = acc;
+  }
+
+  // Last workgroup of this token ranks the logits.
+  __shared__ uint32_t s_last;
+  fence_release();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = atomic_add_acq_rel(&p.ctr[t], 1u);
+    s_last = (prev == gridDim.x - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s_last == 0u || wave != 0) return;
+  fence_acquire();
+
+  constexpr int kMaxPer = kMaxExperts / 64;
+  uint32_t keys[kMaxPer];
+  uint32_t lbits[kMaxPer];
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) {
+    const int e = lane + 64 * i;
+    lbits[i] = 0;
+    keys[i] = 0;
+    if (e < p.E) {
+      const uint32_t b = f32_to_bf16(lg[e]);
+      lbits[i] = b;
+      keys[i] = (bf16_order_key(b) << 16) | (0xFFFFu - (uint32_t)e);
+    }
+  }
+  int my_sel = -1;
+  float my_logit = 0.0f;
+  uint32_t first = 0;
+  for (int j = 0; j < p.K; ++j) {
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i) mine = keys[i] > mine ? keys[i] : mine;
+    const uint32_t best = wave_max_u32(mine);
+    if (j == 0) first = best;
+    const int e = (int)(0xFFFFu - (best & 0xFFFFu));
+#pragma unroll
+    for (int i = 0; i < kMaxPer; ++i)
+      if (lane + 64 * i == e) keys[i] = 0;
+    if (lane == j) {
+      my_sel = e;
+      my_logit = bf16_to_f32(bf16_from_order_key(best >> 16));
+    }
+  }
+  const float m = bf16_to_f32(bf16_from_order_key(first >> 16));
+  float z = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i)
+    if (lane + 64 * i < p.E) z += __expf(bf16_to_f32(lbits[i]) - m);
+  z = wave_sum_butterfly(z);
+  float pb = 0.0f;
+  if (lane < p.K) pb = round_bf16(__expf(my_logit - m) / z);
+  float total = 0.0f;
+  for (int j = 0; j < p.K; ++j) total += __shfl(pb, j, 64);
+  const float score = p.norm ? round_bf16(pb / total) : pb;
+  if (lane < p.K) {
+    p.idx[t * p.K + lane] = my_sel;
+    p.scores[t * (p.K + 1) + lane] = score;
+    if (p.idx_out) p.idx_out[t * p.K + lane] = my_sel;
+    if (p.scores_out) p.scores_out[t * p.K + lane] = score;
+  }
+  if (lane == 0) {
+    float sg = 1.0f;
+    if (has_sg) sg = round_bf16(sigmoid(round_bf16(lg[p.E])));
+    p.scores[t * (p.K + 1) + p.K] = sg;
+    __hip_atomic_store(&p.ctr[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ----------------------------------------------------------------- gate/up
+template <int BITS>
+struct Packing {
+  static constexpr int kValuesPerChunk = BITS == 8 ? 16 : 32;  // per 16 B
+  static constexpr int kValuesPerWord = 32 / BITS;
+};
+
+template <int BITS, int CPL, int PPW>
+__global__ __launch_bounds__(256) void gate_up_kernel(const DecodeArgs p,
+                                                      const int blocks_per_unit) {
+  constexpr int VPC = Packing<BITS>::kValuesPerChunk;
+  const int U1 = p.K + p.has_shared;
+  const int unit = blockIdx.x / blocks_per_unit;
+  const int blk = blockIdx.x - unit * blocks_per_unit;
+  const int t = unit / U1;
+  const int j = unit - t * U1;
+  const bool shared = j >= p.K;
+  const QW q = shared ? p.sgu : p.gu;
+  const int I = p.I;
+  const int e = shared ? 0 : p.idx[t * p.K + j];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int c0 = (blk * 4 + wave) * PPW;
+  if (c0 >= I) return;
+  if (!shared && (unsigned)e >= (unsigned)p.E) {
+    // Caller index outside the bank: the slot contributes zeros and no
+    // weight memory is touched.
+    if (lane < PPW && c0 + lane < I) p.act[(size_t)unit * I + c0 + lane] = 0.0f;
+    return;
+  }
+  const int H = p.H;
+  const int CH = H / VPC;
+  const int WPR = H / Packing<BITS>::kValuesPerWord;
+  const int G = H >> 6;
+
+  float xv[CPL][VPC];
+  float xs[CPL];
+  const uint16_t* xt = p.x + (size_t)t * H;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = lane + 64 * i;
+    xs[i] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < VPC; ++v) xv[i][v] = 0.0f;
+    if (ch < CH) {
+#pragma unroll
+      for (int h = 0; h < VPC / 8; ++h) {
+        const uint4 b = load16(xt + ch * VPC + h * 8);
+        xv[i][h * 8 + 0] = bf16_lo(b.x);
+        xv[i][h * 8 + 1] = bf16_hi(b.x);
+        xv[i][h * 8 + 2] = bf16_lo(b.y);
+        xv[i][h * 8 + 3] = bf16_hi(b.y);
+        xv[i][h * 8 + 4] = bf16_lo(b.z);
+        xv[i][h * 8 + 5] = bf16_hi(b.z);
+        xv[i][h * 8 + 6] = bf16_lo(b.w);
+        xv[i][h * 8 + 7] = bf16_hi(b.w);
+      }
+#pragma unroll
+      for (int v = 0; v < VPC; ++v) xs[i] += xv[i][v];
+    }
+  }
+
+  uint4 wu[PPW][CPL], wg[PPW][CPL];
+  float su[PPW][CPL], bu[PPW][CPL], sg[PPW][CPL], bg[PPW][CPL];
+#pragma unroll
+  for (int pp = 0; pp < PPW; ++pp) {
+    const int c = c0 + pp;
+    const size_t up_row = (size_t)e * 2 * I + (c < I ? c : 0);
+    const size_t gate_row = up_row + I;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = lane + 64 * i;
+      wu[pp][i] = make_uint4(0, 0, 0, 0);
+      wg[pp][i] = make_uint4(0, 0, 0, 0);
+      su[pp][i] = bu[pp][i] = sg[pp][i] = bg[pp][i] = 0.0f;
+      if (c < I && ch < CH) {
+        wu[pp][i] = load16_stream(q.w + up_row * WPR + ch * 4);
+        wg[pp][i] = load16_stream(q.w + gate_row * WPR + ch * 4);
+        const int grp = (ch * VPC) >> 6;
+        su[pp][i] = bf16_to_f32(q.s[up_row * G + grp]);
+        bu[pp][i] = bf16_to_f32(q.b[up_row * G + grp]);
+        sg[pp][i] = bf16_to_f32(q.s[gate_row * G + grp]);
+        bg[pp][i] = bf16_to_f32(q.b[gate_row * G + grp]);
+      }
+    }
+  }
+#pragma unroll
+  for (int pp = 0; pp < PPW; ++pp) {
+    const int c = c0 + pp;
+    if (c >= I) continue;  // wave-uniform
+    float au = 0.0f, ag = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      au += su[pp][i] * qdot_chunk<BITS>(wu[pp][i], xv[i]) + bu[pp][i] * xs[i];
+      ag += sg[pp][i] * qdot_chunk<BITS>(wg[pp][i], xv[i]) + bg[pp][i] * xs[i];
+    }
+    au = wave_sum_butterfly(au);
+    ag = wave_sum_butterfly(ag);
+    if (lane == 0) {
+      const float up = round_bf16(au);
+      const float gate = round_bf16(ag);
+      p.act[(size_t)unit * I + c] = round_bf16(silu(gate) * up);
+    }
+  }
+}
+
+// -------------------------------------------------------------------- down
+// act of the token's units is staged in LDS; every wave owns 64/CHR output
+// rows and loops over the units.  COMBINE: weighted sum + shared expert +
+// optional residual -> out[t, h]; otherwise per-slot rows y[t, j, h].
+template <int BITS, bool COMBINE>
+__global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
+                                                   const int blocks_per_token) {
+  constexpr int VPC = Packing<BITS>::kValuesPerChunk;
+  extern __shared__ float s_act[];
+  const int t = blockIdx.x / blocks_per_token;
+  const int blk = blockIdx.x - t * blocks_per_token;
+  const int U1 = p.K + p.has_shared;
+  const int units = COMBINE ? U1 : p.K;
+  const int I = p.I;
+  const int H = p.H;
+  const float* act_t = p.act + (size_t)t * U1 * I;
+  for (int i = threadIdx.x; i < units * I; i += blockDim.x) s_act[i] = act_t[i];
+  __syncthreads();
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int CHR = I / VPC;  // chunks per row: power of two <= 64
+  const int RPL = 64 / CHR;
+  const int r = lane / CHR;
+  const int ch = lane - r * CHR;
+  const int h0 = (blk * 4 + wave) * RPL;
+  if (h0 >= H) return;
+  const int h = h0 + r;
+  const bool valid = h < H;
+  const int WPR = I / Packing<BITS>::kValuesPerWord;
+  const int G = I >> 6;
+  const int grp = (ch * VPC) >> 6;
+
+  float acc = 0.0f;
+  for (int u0 = 0; u0 < units; u0 += kUnitBatch) {
+    uint4 wv[kUnitBatch];
+    float sv[kUnitBatch], bv[kUnitBatch];
+#pragma unroll
+    for (int b = 0; b < kUnitBatch; ++b) {
+      const int u = u0 + b;
+      wv[b] = make_uint4(0, 0, 0, 0);
+      sv[b] = bv[b] = 0.0f;
+      const bool sh = u >= p.K;
+      const int e = (u < units && !sh) ? p.idx[t * p.K + u] : 0;
+      if (u < units && valid && (unsigned)e < (unsigned)p.E) {
+        const QW q = sh ? p.sdn : p.dn;
+        const size_t row = (size_t)e * H + h;
+        wv[b] = load16_stream(q.w + row * WPR + ch * 4);
+        sv[b] = bf16_to_f32(q.s[row * G + grp]);
+        bv[b] = bf16_to_f32(q.b[row * G + grp]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kUnitBatch; ++b) {
+      const int u = u0 + b;
+      if (u >= units) continue;  // wave-uniform
+      float a[VPC];
+      float asum = 0.0f;
+      const float* src = s_act + u * I + ch * VPC;
+#pragma unroll
+      for (int v = 0; v < VPC; ++v) {
+        a[v] = src[v];
+        asum += a[v];
+      }
+      float y = sv[b] * qdot_chunk<BITS>(wv[b], a) + bv[b] * asum;
+      y = round_bf16(segment_sum(y, CHR));
+      if constexpr (COMBINE) {
+        acc += p.scores[t * (p.K + 1) + u] * y;
+      } else {
+        if (ch == 0 && valid)
+          p.out[((size_t)t * p.K + u) * H + h] = (uint16_t)f32_to_bf16(y);
+      }
+    }
+  }
+  if constexpr (COMBINE) {
+    if (ch == 0 && valid) {
+      float o = round_bf16(acc);
+      if (p.residual) o = round_bf16(bf16_to_f32(p.residual[(size_t)t * H + h]) + o);
+      p.out[(size_t)t * H + h] = (uint16_t)f32_to_bf16(o);
+    }
+  }
+}
+
+// --------------------------------------------------------------------- qmv
+// y[m, n] = x[lhs[m]] . deq(w[rhs[m], n])^T.  Rows of 64/LPR outputs per wave
+// load, where LPR = min(64, chunks per row); CPL chunks per lane.
+template <int BITS, int CPL>
+__global__ __launch_bounds__(256) void qmv_kernel(const QmvArgs p,
+                                                  const int blocks_per_row) {
+  constexpr int VPC = Packing<BITS>::kValuesPerChunk;
+  const int m = blockIdx.x / blocks_per_row;
+  const int blk = blockIdx.x - m * blocks_per_row;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int K = p.K;
+  const int CH = K / VPC;
+  const int LPR = CH >= 64 ? 64 : CH;
+  const int RPL = 64 / LPR;
+  const int r = lane / LPR;
+  const int cl = lane - r * LPR;
+  const int n = (blk * 4 + wave) * RPL + r;
+  if ((blk * 4 + wave) * RPL >= p.N) return;
+  const bool valid = n < p.N;
+  int xrow = p.lhs ? p.lhs[m] : m;
+  int e = p.rhs ? p.rhs[m] : 0;
+  const bool in_range =
+      (unsigned)xrow < (unsigned)p.x_rows && (unsigned)e < (unsigned)p.experts;
+  if (!in_range) xrow = e = 0;  // row of zeros, no out-of-range access
+  const uint16_t* xr = p.x + (size_t)xrow * K;
+  const size_t row = (size_t)e * p.N + (valid ? n : 0);
+  const int WPR = K / Packing<BITS>::kValuesPerWord;
+  const int G = K >> 6;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = cl + LPR * i;
+    if (ch < CH && valid && in_range) {
+      const uint4 wv = load16_stream(p.w.w + row * WPR + ch * 4);
+      float a[VPC];
+      float asum = 0.0f;
+#pragma unroll
+      for (int h = 0; h < VPC / 8; ++h) {
+        const uint4 b = load16(xr + ch * VPC + h * 8);
+        a[h * 8 + 0] = bf16_lo(b.x);
+        a[h * 8 + 1] = bf16_hi(b.x);
+        a[h * 8 + 2] = bf16_lo(b.y);
+        a[h * 8 + 3] = bf16_hi(b.y);
+        a[h * 8 + 4] = bf16_lo(b.z);
+        a[h * 8 + 5] = bf16_hi(b.z);
+        a[h * 8 + 6] = bf16_lo(b.w);
+        a[h * 8 + 7] = bf16_hi(b.w);
+      }
+#pragma unroll
+      for (int v = 0; v < VPC; ++v) asum += a[v];
+      const int grp = (ch * VPC) >> 6;
+      acc += bf16_to_f32(p.w.s[row * G + grp]) * qdot_chunk<BITS>(wv, a) +
+             bf16_to_f32(p.w.b[row * G + grp]) * asum;
+    }
+  }
+  acc = segment_sum(acc, LPR);
+  if (cl == 0 && valid) {
+    if (p.y_f32)
+      p.y_f32[(size_t)m * p.N + n] = acc;
+    else
+      p.y_bf16[(size_t)m * p.N + n] = (uint16_t)f32_to_bf16(acc);
+  }
+}
+
+// ------------------------------------------------------------------ launch
+#define RMOE_CHECK_LAUNCH()                  \
+  do {                                       \
+    hipError_t _e = hipGetLastError();       \
+    if (_e != hipSuccess) return _e;         \
+  } while (0)
+
+hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
+  const int rows = a.E + (a.sgate_w ? 1 : 0);
+  dim3 grid((rows + 3) / 4, a.T);
+  hipLaunchKernelGGL(router_kernel, grid, dim3(256), 0, s, a);
+  RMOE_CHECK_LAUNCH();
+  return hipSuccess;
+}
+
+template <int BITS, int CPL>
+static hipError_t gate_up_cpl(const DecodeArgs& a, hipStream_t s) {
+  constexpr int PPW = 2;
+  const int U1 = a.K + a.has_shared;
+  const int bpu = (a.I + 4 * PPW - 1) / (4 * PPW);
+  const long long blocks = (long long)bpu * U1 * a.T;
+  hipLaunchKernelGGL((gate_up_kernel<BITS, CPL, PPW>), dim3((unsigned)blocks),
+                     dim3(256), 0, s, a, bpu);
+  RMOE_CHECK_LAUNCH();
+  return hipSuccess;
+}
+
+hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s) {
+  const int vpc = bits == 8 ? 16 : 32;
+  const int cpl = (a.H / vpc + 63) / 64;
+  if (bits == 8) {
+    if (cpl <= 1) return gate_up_cpl<8, 1>(a, s);
+    if (cpl <= 2) return gate_up_cpl<8, 2>(a, s);
+    return gate_up_cpl<8, 4>(a, s);
+  }
+  if (cpl <= 1) return gate_up_cpl<4, 1>(a, s);
+  if (cpl <= 2) return gate_up_cpl<4, 2>(a, s);
+  return gate_up_cpl<4, 4>(a, s);
+}
+
+hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s) {
+  const int vpc = bits == 8 ? 16 : 32;
+  const int rpl = 64 / (a.I / vpc);
+  const int bpt = (a.H + 4 * rpl - 1) / (4 * rpl);
+  const int units = combine ? a.K + a.has_shared : a.K;
+  const size_t lds = (size_t)units * a.I * sizeof(float);
+  dim3 grid((unsigned)((long long)bpt * a.T));
+  if (bits == 8) {
+    if (combine)
+      hipLaunchKernelGGL((down_kernel<8, true>), grid, dim3(256), lds, s, a, bpt);
+    else
+      hipLaunchKernelGGL((down_kernel<8, false>), grid, dim3(256), lds, s, a, bpt);
+  } else {
+    if (combine)
+      hipLaunchKernelGGL((down_kernel<4, true>), grid, dim3(256), lds, s, a, bpt);
+    else
+      hipLaunchKernelGGL((down_kernel<4, false>), grid, dim3(256), lds, s, a, bpt);
+  }
+  RMOE_CHECK_LAUNCH();
+  return hipSuccess;
+}
+
+template <int BITS, int CPL>
+static hipError_t qmv_cpl(const QmvArgs& a, hipStream_t s) {
+  const int vpc = BITS == 8 ? 16 : 32;
+  const int ch = a.K / vpc;
+  const int lpr = ch >= 64 ? 64 : ch;
+  const int rows_per_block = 4 * (64 / lpr);
+  const int bpr = (a.N + rows_per_block - 1) / rows_per_block;
+  const long long blocks = (long long)bpr * a.M;
+  hipLaunchKernelGGL((qmv_kernel<BITS, CPL>), dim3((unsigned)blocks), dim3(256),
+                     0, s, a, bpr);
+  RMOE_CHECK_LAUNCH();
+  return hipSuccess;
+}
+
+hipError_t launch_qmv(const QmvArgs& a, int bits, hipStream_t s) {
+  const int vpc = bits == 8 ? 16 : 32;
+  const int cpl = (a.K / vpc + 63) / 64;
+  if (bits == 8) {
+    if (cpl <= 1) return qmv_cpl<8, 1>(a, s);
+    if (cpl <= 2) return qmv_cpl<8, 2>(a, s);
+    return qmv_cpl<8, 4>(a, s);
+  }
+  if (cpl <= 1) return qmv_cpl<4, 1>(a, s);
+  if (cpl <= 2) return qmv_cpl<4, 2>(a, s);
+  return qmv_cpl<4, 4>(a, s);
+}
+
+}  // namespace rmoe

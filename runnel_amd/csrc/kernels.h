@@ -1,0 +1,66 @@
+// Launch-side view of the kernels: argument blocks and launchers.  Host code
+// (abi.cpp) validates every shape before calling a launcher.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rmoe {
+
+constexpr int kMaxExperts = 1024;  // router ranks at most this many experts
+constexpr int kMaxTopK = 64;       // one slot per lane in the ranking wave
+constexpr int kUnitBatch = 9;      // down kernel: loads in flight per lane
+constexpr int kMaxTokens = 65535;  // grid.y of the router; counters reserved
+
+struct QW {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+};
+
+// One decode-shaped call: T tokens, K routed slots, an optional shared
+// expert (unit K of every token).
+struct DecodeArgs {
+  int T, H, I, E, K, has_shared, norm;
+  int switch_mode;   // 1: idx are caller indices, range-checked per use
+  const uint16_t* x;
+  const uint16_t* router_w;
+  const uint16_t* sgate_w;
+  QW gu, dn, sgu, sdn;
+  float* logits;     // [T, E + 1]
+  int32_t* idx;      // [T, K]   (switch path: caller's indices)
+  float* scores;     // [T, K + 1] (slot K: shared sigmoid gate)
+  float* act;        // [T, K + has_shared, I]
+  uint32_t* ctr;     // [T] zero between calls
+  uint16_t* out;     // [T, H] (block) or [T, K, H] (switch)
+  const uint16_t* residual;
+  int32_t* idx_out;
+  float* scores_out;
+};
+
+struct QmvArgs {
+  int M, N, K;
+  int x_rows, experts;  // lhs / rhs outside [0, x_rows) / [0, experts) -> zero row
+  const uint16_t* x;
+  const int32_t* lhs;
+  const int32_t* rhs;
+  QW w;
+  uint16_t* y_bf16;
+  float* y_f32;
+};
+
+hipError_t launch_router(const DecodeArgs& a, hipStream_t s);
+hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s);
+hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s);
+hipError_t launch_qmv(const QmvArgs& a, int bits, hipStream_t s);
+
+hipError_t launch_quantize(const float* w, int64_t rows, int cols, int bits,
+                           uint32_t* wq, uint16_t* s, uint16_t* b, hipStream_t st);
+hipError_t launch_dequantize(const QW& q, int cols, int bits, int64_t row_begin,
+                             int64_t rows, float* out_f32, uint16_t* out_bf16,
+                             hipStream_t st);
+hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* partials,
+                              int blocks, hipStream_t st);
+
+}  // namespace rmoe

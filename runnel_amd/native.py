@@ -1,0 +1,277 @@
+"""torch-facing wrappers over the C ABI (include/rmoe.h).
+
+Every function here hands device pointers of torch tensors to librmoe.so
+and enqueues the HIP kernels on torch's current stream; nothing computes on
+the host.  Packed weights are carried as int32 tensors (the same bits as
+MLX's uint32 words); scales, biases and activations as bfloat16.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+
+
+def _require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("runnel_amd kernels take GPU tensors")
+
+
+def values_per_word(bits: int) -> int:
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8 (got {bits})")
+    return 32 // bits
+
+
+def qweight_struct(weight, scales, biases, bits: int, group_size: int = 64) -> _lib.QWeight:
+    """rmoe_qweight for a bank [E, rows, K*bits/32] (or a matrix without the
+    expert axis)."""
+    if weight.dim() == 2:
+        experts, rows, words = 1, weight.shape[0], weight.shape[1]
+    elif weight.dim() == 3:
+        experts, rows, words = weight.shape
+    else:
+        raise ValueError("packed weight must be 2-D or 3-D")
+    for t, name in ((weight, "weight"), (scales, "scales"), (biases, "biases")):
+        if t is None:
+            raise ValueError(f"{name} is required")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if weight.dtype not in (torch.int32, getattr(torch, "uint32", torch.int32)):
+        raise ValueError("packed weight must be int32/uint32")
+    if scales.dtype != BF16 or biases.dtype != BF16:
+        raise ValueError("scales and biases must be bfloat16")
+    cols = words * values_per_word(bits)
+    return _lib.QWeight(weight.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                        experts, rows, cols, bits, group_size)
+
+
+class Workspace:
+    """Grow-only, zero-initialised device scratch per (device, purpose).
+    The library keeps its counters at zero between calls, so the buffer is
+    zeroed only when it is (re)allocated."""
+
+    def __init__(self):
+        self._bufs: dict = {}
+
+    def get(self, device, nbytes: int, key: str = "default") -> torch.Tensor:
+        k = (str(device), key)
+        buf = self._bufs.get(k)
+        if buf is None or buf.numel() < nbytes:
+            # 256-byte alignment comes from the caching allocator (512 B).
+            buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._bufs[k] = buf
+        return buf
+
+
+WORKSPACE = Workspace()
+
+
+def gather_qmm(x: torch.Tensor, weight, scales, biases, bits: int, group_size: int = 64,
+               rhs_indices: torch.Tensor | None = None,
+               lhs_indices: torch.Tensor | None = None,
+               out_dtype=BF16) -> torch.Tensor:
+    """y[m] = x[lhs[m]] @ dequantize(weight[rhs[m]]).T  (mx.gather_qmm with
+    transpose=True, called at src/runnel/mlx.py:64-75).
+
+    x: bf16 [x_rows, K]; rhs_indices / lhs_indices: int32 [M] (None: expert
+    0 / row m).  Returns [M, N] in bf16 or float32."""
+    lib = _lib.load()
+    _require_cuda(x, weight, rhs_indices, lhs_indices)
+    if x.dtype != BF16 or x.dim() != 2:
+        raise ValueError("x must be a 2-D bfloat16 tensor")
+    x = x.contiguous()
+    qw = qweight_struct(weight, scales, biases, bits, group_size)
+    if lhs_indices is not None:
+        lhs_indices = lhs_indices.to(torch.int32).contiguous()
+        M = lhs_indices.numel()
+    elif rhs_indices is not None:
+        M = rhs_indices.numel()
+    else:
+        M = x.shape[0]
+    if rhs_indices is not None:
+        rhs_indices = rhs_indices.to(torch.int32).contiguous()
+        if rhs_indices.numel() != M:
+            raise ValueError("rhs_indices must have one entry per output row")
+    if lhs_indices is None and x.shape[0] != M:
+        raise ValueError("x must have one row per output row when lhs_indices is None")
+    y = torch.empty((M, qw.rows), dtype=out_dtype, device=x.device)
+    if out_dtype not in (BF16, torch.float32):
+        raise ValueError("out_dtype must be bfloat16 or float32")
+    _lib.check(lib.rmoe_gather_qmm(
+        x.data_ptr(), x.shape[0], _lib.ptr(lhs_indices), _lib.ptr(rhs_indices), M,
+        ctypes.byref(qw), y.data_ptr() if out_dtype == BF16 else None,
+        y.data_ptr() if out_dtype == torch.float32 else None,
+        _lib.stream_handle(x.device)))
+    return y
+
+
+def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate_up: _lib.QWeight,
+               down: _lib.QWeight) -> torch.Tensor:
+    """Packed [up; gate] projection + SwiGLU + down per (token, slot):
+    x bf16 [T, H], indices int [T, k] -> bf16 [T, k, H] (uncombined)."""
+    lib = _lib.load()
+    _require_cuda(x, indices)
+    x = x.contiguous()
+    idx = indices.to(torch.int32).contiguous()
+    T, k = idx.shape
+    H = gate_up.cols
+    y = torch.empty((T, k, H), dtype=BF16, device=x.device)
+    need = lib.rmoe_switch_workspace_bytes(ctypes.byref(gate_up), ctypes.byref(down), T, k)
+    ws = WORKSPACE.get(x.device, need, "switch")
+    _lib.check(lib.rmoe_switch_glu(ctypes.byref(gate_up), ctypes.byref(down),
+                                   x.data_ptr(), T, idx.data_ptr(), k, y.data_ptr(),
+                                   ws.data_ptr(), ws.numel(),
+                                   _lib.stream_handle(x.device)))
+    return y
+
+
+@dataclass
+class LayerHandle:
+    """An rmoe_layer struct plus the tensors it points at (kept alive)."""
+    struct: _lib.Layer
+    tensors: tuple
+
+    @property
+    def hidden(self):
+        return self.struct.hidden
+
+    @property
+    def top_k(self):
+        return self.struct.top_k
+
+    def workspace_bytes(self, tokens: int) -> int:
+        return _lib.load().rmoe_workspace_bytes(ctypes.byref(self.struct), tokens)
+
+    def validate(self):
+        _lib.check(_lib.load().rmoe_validate_layer(ctypes.byref(self.struct)))
+
+
+def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
+               shared_gate_w=None, shared_gate_up=None, shared_down=None,
+               bits: int = 8, group_size: int = 64) -> LayerHandle:
+    """router_w bf16 [E, H]; gate_up / down / shared_* are (weight, scales,
+    biases) triples of packed banks; shared banks may omit the expert axis."""
+    gu = qweight_struct(*gate_up, bits, group_size)
+    dn = qweight_struct(*down, bits, group_size)
+    keep = [router_w, *gate_up, *down]
+    if shared_gate_up is not None:
+        sgu = qweight_struct(*shared_gate_up, bits, group_size)
+        sdn = qweight_struct(*shared_down, bits, group_size)
+        keep += [*shared_gate_up, *shared_down]
+        shared_inter = sgu.rows // 2
+    else:
+        sgu = _lib.QWeight()
+        sdn = _lib.QWeight()
+        shared_inter = 0
+    if shared_gate_w is not None:
+        shared_gate_w = shared_gate_w.reshape(-1).contiguous()
+        keep.append(shared_gate_w)
+    if router_w.dtype != BF16 or not router_w.is_contiguous():
+        raise ValueError("router weight must be contiguous bfloat16 [experts, hidden]")
+    s = _lib.Layer(router_w.shape[1], gu.rows // 2, shared_inter, router_w.shape[0],
+                   top_k, int(bool(norm_topk_prob)), router_w.data_ptr(),
+                   _lib.ptr(shared_gate_w), gu, dn, sgu, sdn)
+    h = LayerHandle(s, tuple(keep))
+    h.validate()
+    return h
+
+
+def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None = None,
+              out: torch.Tensor | None = None, return_routing: bool = False,
+              workspace: torch.Tensor | None = None):
+    """Whole SparseMoeBlock on x bf16 [T, H] -> bf16 [T, H]."""
+    lib = _lib.load()
+    _require_cuda(x, residual, out)
+    if x.dtype != BF16 or x.dim() != 2:
+        raise ValueError("x must be a 2-D bfloat16 tensor")
+    x = x.contiguous()
+    T = x.shape[0]
+    if out is None:
+        out = torch.empty_like(x)
+    idx = scores = None
+    if return_routing:
+        idx = torch.empty((T, layer.top_k), dtype=torch.int32, device=x.device)
+        scores = torch.empty((T, layer.top_k), dtype=torch.float32, device=x.device)
+    need = layer.workspace_bytes(T)
+    ws = workspace if workspace is not None else WORKSPACE.get(x.device, need, "block")
+    _lib.check(lib.rmoe_moe_block(ctypes.byref(layer.struct), x.data_ptr(), T,
+                                  _lib.ptr(residual), out.data_ptr(), _lib.ptr(idx),
+                                  _lib.ptr(scores), ws.data_ptr(), ws.numel(),
+                                  _lib.stream_handle(x.device)))
+    if return_routing:
+        return out, idx, scores
+    return out
+
+
+def router(router_w: torch.Tensor, x: torch.Tensor, top_k: int,
+           norm_topk_prob: bool = True):
+    """Router of the block: x bf16 [T, H], router_w bf16 [E, H] ->
+    (indices int32 [T, k] in rank order, scores float32 [T, k])."""
+    lib = _lib.load()
+    _require_cuda(x, router_w)
+    x = x.contiguous()
+    router_w = router_w.contiguous()
+    T, H = x.shape
+    E = router_w.shape[0]
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+    scores = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    need = lib.rmoe_router_workspace_bytes(E, top_k, T)
+    ws = WORKSPACE.get(x.device, need, "router")
+    _lib.check(lib.rmoe_router(router_w.data_ptr(), E, H, top_k, int(bool(norm_topk_prob)),
+                               x.data_ptr(), T, idx.data_ptr(), scores.data_ptr(),
+                               ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device)))
+    return idx, scores
+
+
+def quantize(w: torch.Tensor, bits: int, group_size: int = 64):
+    """Affine quantization of float32 [..., K] on the GPU ->
+    (int32 words [..., K*bits/32], bf16 scales, bf16 biases)."""
+    lib = _lib.load()
+    _require_cuda(w)
+    if w.dtype != torch.float32:
+        raise ValueError("quantize takes float32 weights")
+    w = w.contiguous()
+    K = w.shape[-1]
+    lead = w.shape[:-1]
+    rows = w.numel() // K
+    wq = torch.empty((*lead, K // values_per_word(bits)), dtype=torch.int32, device=w.device)
+    s = torch.empty((*lead, K // group_size), dtype=BF16, device=w.device)
+    b = torch.empty_like(s)
+    _lib.check(lib.rmoe_quantize(w.data_ptr(), rows, K, bits, group_size, wq.data_ptr(),
+                                 s.data_ptr(), b.data_ptr(), _lib.stream_handle(w.device)))
+    return wq, s, b
+
+
+def dequantize(weight, scales, biases, bits: int, group_size: int = 64,
+               out_dtype=torch.float32) -> torch.Tensor:
+    """fl32(q*s + b) for every element ([..., K]); bf16 output rounds that
+    value to nearest-even."""
+    lib = _lib.load()
+    _require_cuda(weight)
+    qw = qweight_struct(weight, scales, biases, bits, group_size)
+    rows = qw.experts * qw.rows
+    out = torch.empty((*weight.shape[:-1], qw.cols), dtype=out_dtype, device=weight.device)
+    _lib.check(lib.rmoe_dequantize(
+        ctypes.byref(qw), 0, rows,
+        out.data_ptr() if out_dtype == torch.float32 else None,
+        out.data_ptr() if out_dtype == BF16 else None,
+        _lib.stream_handle(weight.device)))
+    return out
+
+
+def stream_read(buf: torch.Tensor, blocks: int, partials: torch.Tensor | None = None):
+    lib = _lib.load()
+    nbytes = buf.numel() * buf.element_size()
+    if partials is None:
+        partials = torch.empty(blocks, dtype=torch.int32, device=buf.device)
+    _lib.check(lib.rmoe_stream_read(buf.data_ptr(), nbytes, partials.data_ptr(), blocks,
+                                    _lib.stream_handle(buf.device)))
+    return partials

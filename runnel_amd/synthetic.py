@@ -1,0 +1,89 @@
+"""Synthetic MoE layers generated on the GPU.
+
+Weights are drawn from N(0, std) with a seeded torch generator on the
+device, quantized by the HIP quantizer (rmoe_quantize) in chunks, and kept
+resident: a 256-expert 8-bit layer is 0.86 GB, so the 40-layer stack is
+34 GB of HBM.  The router and the shared-expert gate stay bf16.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import native
+
+BF16 = torch.bfloat16
+
+
+@dataclass
+class LayerWeights:
+    router_w: torch.Tensor        # bf16 [E, H]
+    gate_up: tuple                # (int32 [E, 2I, H/vpw], bf16 [E, 2I, H/64] x2)
+    down: tuple                   # (int32 [E, H, I/vpw], ...)
+    shared_gate_w: torch.Tensor | None
+    shared_gate_up: tuple | None  # [2Is, H/vpw] ...
+    shared_down: tuple | None
+    bits: int
+    top_k: int
+    norm_topk_prob: bool = True
+
+    def handle(self) -> native.LayerHandle:
+        return native.make_layer(self.router_w, self.gate_up, self.down, self.top_k,
+                                 self.norm_topk_prob, self.shared_gate_w,
+                                 self.shared_gate_up, self.shared_down, self.bits)
+
+    def tensors(self):
+        ts = [self.router_w, *self.gate_up, *self.down]
+        if self.shared_gate_up is not None:
+            ts += [self.shared_gate_w, *self.shared_gate_up, *self.shared_down]
+        return ts
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self.tensors())
+
+
+def _quantized_bank(gen, experts, rows, cols, bits, std, device, chunk_rows=1 << 16):
+    vpw = native.values_per_word(bits)
+    total = experts * rows
+    w = torch.empty((total, cols // vpw), dtype=torch.int32, device=device)
+    s = torch.empty((total, cols // 64), dtype=BF16, device=device)
+    b = torch.empty_like(s)
+    for r0 in range(0, total, chunk_rows):
+        r1 = min(total, r0 + chunk_rows)
+        f = torch.randn((r1 - r0, cols), generator=gen, device=device, dtype=torch.float32)
+        f.mul_(std)
+        wq, sq, bq = native.quantize(f, bits)
+        w[r0:r1].copy_(wq)
+        s[r0:r1].copy_(sq)
+        b[r0:r1].copy_(bq)
+        del f, wq, sq, bq
+    shape = (experts, rows) if experts > 1 else (rows,)
+    return (w.reshape(*shape, -1), s.reshape(*shape, -1), b.reshape(*shape, -1))
+
+
+def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8, bits=8,
+               shared=True, std=0.02, router_std=0.02, device="cuda",
+               shared_inter=None) -> LayerWeights:
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    shared_inter = inter if shared_inter is None else shared_inter
+    router = (torch.randn((experts, hidden), generator=gen, device=device) * router_std).to(BF16)
+    gu = _quantized_bank(gen, experts, 2 * inter, hidden, bits, std, device)
+    dn = _quantized_bank(gen, experts, hidden, inter, bits, std, device)
+    if gu[0].dim() == 2:  # experts == 1 keeps the expert axis for banks
+        gu = tuple(t.unsqueeze(0) for t in gu)
+        dn = tuple(t.unsqueeze(0) for t in dn)
+    sg = sgu = sdn = None
+    if shared:
+        sg = (torch.randn((hidden,), generator=gen, device=device) * router_std).to(BF16)
+        sgu = _quantized_bank(gen, 1, 2 * shared_inter, hidden, bits, std, device)
+        sdn = _quantized_bank(gen, 1, hidden, shared_inter, bits, std, device)
+    return LayerWeights(router, gu, dn, sg, sgu, sdn, bits, top_k)
+
+
+def make_x(seed: int, tokens: int, hidden: int, device="cuda") -> torch.Tensor:
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    return torch.randn((tokens, hidden), generator=gen, device=device).to(BF16)
