@@ -144,6 +144,27 @@ int rmoe_moe_block(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
                    int32_t* indices_out, float* scores_out, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Batch-1 decode of one token through a stack of MoE layers with a residual
+ * add between them: x_{l+1} = bf16(x_l + block_l(x_l)), one launch for the
+ * whole stack (the chained decode of the reference's 40-layer model,
+ * docs/architecture.md:31-37; there is no single reference entry point).
+ * The layer descriptors are packed once on the host with
+ * rmoe_chain_table_pack into rmoe_chain_table_bytes(n) bytes, copied by the
+ * caller to device memory, and passed as device_table; layer0 describes the
+ * common shape.  Needs hidden 2048, inter 512, top_k + shared <= 9,
+ * experts <= 512.  x, out bf16 [hidden]. */
+size_t rmoe_chain_table_bytes(int32_t n_layers);
+int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers,
+                          void* host_table);
+int rmoe_moe_chain(const rmoe_layer* layer0, const void* device_table,
+                   int32_t n_layers, const uint16_t* x, uint16_t* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Byte offset inside a workspace of a uint32 status word: nonzero when a
+ * single-launch decode timed out waiting for another workgroup (the call
+ * still completes; its outputs are then not valid). */
+size_t rmoe_workspace_status_offset(void);
+
 /* Affine quantization of fp32 rows [rows, cols] (group_size 64, bits 4|8):
  * per group, the larger-magnitude edge value is kept exact, scale and bias
  * are rounded to bf16 and the codes are round-half-even((w - b) / s)

@@ -346,7 +346,7 @@ typedef struct {
  * The reduction axis is cut into 8-element chunks; lane l of a 64-lane
  * wavefront sums chunks l, l+64, l+128, ... in order, element by element,
  * starting from +0.0f; the 64 lane sums are then combined by a butterfly
- * p_l <- p_l + p_{l xor d} for d = 32, 16, 8, 4, 2, 1.  Products of two bf16
+ * p_l <- p_l + p_{l xor d} for d = 1, 2, 4, 8, 16, 32.  Products of two bf16
  * values are exact in fp32, so fused and unfused multiply-add agree.
  */
 float orc_router_dot(const uint16_t* x, const uint16_t* w, int hidden) {
@@ -359,7 +359,7 @@ float orc_router_dot(const uint16_t* x, const uint16_t* w, int hidden) {
         acc += orc_bf16_to_f32(x[c * 8 + j]) * orc_bf16_to_f32(w[c * 8 + j]);
     p[l] = acc;
   }
-  for (int d = 32; d >= 1; d >>= 1) {
+  for (int d = 1; d <= 32; d <<= 1) {
     float q[64];
     for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ d];
     memcpy(p, q, sizeof(p));
@@ -398,19 +398,12 @@ static void group_sums(const float* v, int n, int group, float* out) {
 
 static float silu(float g) { return g / (1.0f + expf(-g)); }
 
-/* y[h] = bf16(down(bf16(silu(bf16(gate)) * bf16(up)))) for one expert. */
-static void expert_ffn(const orc_qweight* gu, const orc_qweight* dn,
-                       size_t expert, int inter, int hidden, const float* xv,
-                       const float* xsum, float* y, float* act, float* asum) {
-  for (int c = 0; c < inter; ++c) {
-    const float up = round_bf16(qdot(gu, expert, (size_t)c, xv, xsum));
-    const float gate =
-        round_bf16(qdot(gu, expert, (size_t)(inter + c), xv, xsum));
-    act[c] = round_bf16(silu(gate) * up);
-  }
-  group_sums(act, inter, dn->group, asum);
-  for (int h = 0; h < hidden; ++h)
-    y[h] = round_bf16(qdot(dn, expert, (size_t)h, act, asum));
+/* act[c] = bf16(silu(bf16(gate_c)) * bf16(up_c)) for one expert row pair. */
+static float expert_act(const orc_qweight* gu, size_t expert, int inter, int c,
+                        const float* xv, const float* xsum) {
+  const float up = round_bf16(qdot(gu, expert, (size_t)c, xv, xsum));
+  const float gate = round_bf16(qdot(gu, expert, (size_t)(inter + c), xv, xsum));
+  return round_bf16(silu(gate) * up);
 }
 
 /*
@@ -487,43 +480,51 @@ int orc_moe_block(const orc_layer* L, const uint16_t* x, int T,
     }
     float* xv = (float*)malloc((size_t)H * sizeof(float));
     float* xsum = (float*)malloc((size_t)H * sizeof(float));
-    float* y = (float*)malloc((size_t)(K + 1) * H * sizeof(float));
-    if (!xv || !xsum || !y) {
-      free(xv); free(xsum); free(y);
+    const int n_units = K + has_shared;
+    float* act = (float*)malloc((size_t)n_units * maxI * sizeof(float));
+    float* asum = (float*)malloc((size_t)n_units * maxI * sizeof(float));
+    if (!xv || !xsum || !act || !asum) {
+      free(xv); free(xsum); free(act); free(asum);
       return ORC_EINVAL;
     }
     for (int h = 0; h < H; ++h) xv[h] = orc_bf16_to_f32(xt[h]);
     group_sums(xv, H, L->gate_up.group, xsum);
-    const int n_units = K + has_shared;
-    /* Each expert's gate/up rows and each block of down rows are independent;
-     * parallelise over (unit, row block) without changing per-row order. */
-#pragma omp parallel
-    {
-      float* act = (float*)malloc((size_t)maxI * sizeof(float));
-      float* asum = (float*)malloc((size_t)maxI * sizeof(float));
-#pragma omp for schedule(static)
-      for (int u = 0; u < n_units; ++u) {
-        if (u < K)
-          expert_ffn(&L->gate_up, &L->down, (size_t)idx[u], I, H, xv, xsum,
-                     y + (size_t)u * H, act, asum);
-        else
-          expert_ffn(&L->shared_gate_up, &L->shared_down, 0, Is, H, xv, xsum,
-                     y + (size_t)u * H, act, asum);
+    /* Gate/up rows of every unit, then the down rows; each output value is
+     * computed by one thread in the same order whatever the thread count. */
+#pragma omp parallel for schedule(static)
+    for (int uc = 0; uc < n_units * maxI; ++uc) {
+      const int u = uc / maxI, c = uc % maxI;
+      if (u < K) {
+        if (c < I) act[(size_t)u * maxI + c] = expert_act(&L->gate_up, (size_t)idx[u], I, c, xv, xsum);
+      } else if (c < Is) {
+        act[(size_t)u * maxI + c] = expert_act(&L->shared_gate_up, 0, Is, c, xv, xsum);
       }
-      free(act);
-      free(asum);
     }
+    for (int u = 0; u < n_units; ++u) {
+      const int Iu = u < K ? I : Is;
+      group_sums(act + (size_t)u * maxI, Iu, L->down.group, asum + (size_t)u * maxI);
+    }
+#pragma omp parallel for schedule(static)
     for (int h = 0; h < H; ++h) {
       float acc = 0.0f;
-      for (int j = 0; j < K; ++j) acc += scores[j] * y[(size_t)j * H + h];
-      if (has_shared) acc += sgate * y[(size_t)K * H + h];
+      for (int j = 0; j < K; ++j) {
+        const float y = round_bf16(qdot(&L->down, (size_t)idx[j], (size_t)h,
+                                        act + (size_t)j * maxI, asum + (size_t)j * maxI));
+        acc += scores[j] * y;
+      }
+      if (has_shared) {
+        const float y = round_bf16(qdot(&L->shared_down, 0, (size_t)h,
+                                        act + (size_t)K * maxI, asum + (size_t)K * maxI));
+        acc += sgate * y;
+      }
       float o = round_bf16(acc);
       if (residual) o = round_bf16(orc_bf16_to_f32(residual[(size_t)t * H + h]) + o);
       out[(size_t)t * H + h] = orc_f32_to_bf16(o);
     }
     free(xv);
     free(xsum);
-    free(y);
+    free(act);
+    free(asum);
   }
   return ORC_OK;
 }

@@ -177,7 +177,7 @@ def router_logits(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
     x_bits [T, H], w_bits [E, H] (bf16 bits) -> float32 [T, E] (not rounded).
     The reduction axis is cut into 8-element chunks; lane l of 64 sums chunks
     l, l+64, ... element by element from +0.0; the lane sums are combined by
-    the butterfly p_l <- p_l + p_(l xor d), d = 32, 16, 8, 4, 2, 1.  The
+    the butterfly p_l <- p_l + p_(l xor d), d = 1, 2, 4, 8, 16, 32.  The
     products of two bf16 values are exact in float32.
     """
     x = bf16_to_f32(x_bits)
@@ -198,7 +198,7 @@ def router_logits(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
             k = cv * 8 + j
             prod = x[:, None, k] * w[None, :, k]  # [T, E, 64], exact
             p = np.where(valid[None, None, :], p + prod, p).astype(np.float32)
-    for d in (32, 16, 8, 4, 2, 1):
+    for d in (1, 2, 4, 8, 16, 32):
         p = (p + p[:, :, lanes ^ d]).astype(np.float32)
     return p[:, :, 0]
 

@@ -28,7 +28,8 @@ EXPORTED = (
     "rmoe_validate_layer", "rmoe_workspace_bytes", "rmoe_router",
     "rmoe_switch_glu", "rmoe_switch_workspace_bytes", "rmoe_gather_qmm",
     "rmoe_moe_block", "rmoe_quantize", "rmoe_dequantize", "rmoe_stream_read",
-    "rmoe_router_workspace_bytes",
+    "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes", "rmoe_chain_table_pack",
+    "rmoe_moe_chain", "rmoe_workspace_status_offset",
 )
 
 
@@ -105,10 +106,17 @@ def load() -> ctypes.CDLL:
         lib.rmoe_quantize.argtypes = [P, I64, I32, I32, I32, P, P, P, P]
         lib.rmoe_dequantize.argtypes = [QP, I64, I64, P, P, P]
         lib.rmoe_stream_read.argtypes = [P, SZ, P, I32, P]
+        lib.rmoe_chain_table_bytes.restype = SZ
+        lib.rmoe_chain_table_bytes.argtypes = [I32]
+        lib.rmoe_chain_table_pack.argtypes = [LP, I32, P]
+        lib.rmoe_moe_chain.argtypes = [LP, P, I32, P, P, P, SZ, P]
+        lib.rmoe_workspace_status_offset.restype = SZ
+        lib.rmoe_workspace_status_offset.argtypes = []
         for name in EXPORTED:
             if name not in ("rmoe_last_error", "rmoe_status_string",
                             "rmoe_workspace_bytes", "rmoe_switch_workspace_bytes",
-                            "rmoe_router_workspace_bytes"):
+                            "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes",
+                            "rmoe_workspace_status_offset"):
                 getattr(lib, name).restype = ctypes.c_int
         if lib.rmoe_abi_version() != ABI_VERSION:
             raise RuntimeError("librmoe.so ABI version mismatch; rebuild it")

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <string>
 
@@ -133,7 +134,7 @@ size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Workspace carve-up shared by the router, switch and block calls.
 struct Layout {
-  size_t logits, idx, scores, act, ctr, total;
+  size_t ctr, fused, logits, idx, scores, act, total;
 };
 
 // The per-token counters sit at a fixed offset with room for the largest
@@ -144,6 +145,8 @@ Layout layout(int T, int E, int K, int I) {
   size_t off = 0;
   l.ctr = off;
   off = align_up(off + (size_t)(rmoe::kMaxTokens + 1) * sizeof(uint32_t));
+  l.fused = off;
+  off = align_up(off + sizeof(rmoe::FusedScratch));
   l.logits = off;
   off = align_up(off + (size_t)T * (E + 1) * sizeof(float));
   l.idx = off;
@@ -200,6 +203,52 @@ rmoe::DecodeArgs decode_args(const rmoe_layer* L, const uint16_t* x, int T,
   a.act = reinterpret_cast<float*>(base + l.act);
   a.ctr = reinterpret_cast<uint32_t*>(base + l.ctr);
   return a;
+}
+
+// The single-launch decode kernel is specialised for the block's native
+// shape and needs one resident workgroup per CU with enough waves to give
+// every down row its own wave.
+bool fused_eligible(const rmoe_layer* L, int* grid) {
+  const int units = L->top_k + (L->shared_gate_up.w ? 1 : 0);
+  if (L->hidden != rmoe::kFusedH || L->inter != rmoe::kFusedI) return false;
+  if (units > rmoe::kMaxFusedUnits || L->experts > rmoe::kFusedMaxExperts) return false;
+  int g = 0;
+  if (rmoe::fused_grid(L->gate_up.bits, &g) != hipSuccess) return false;
+  const int waves = g * (rmoe::kFusedThreads / 64);
+  if (waves < rmoe::kFusedH * 1 / rmoe::kMaxFusedRowsPerWave) return false;
+  if ((units * rmoe::kFusedI + waves - 1) / waves > rmoe::kMaxFusedPairsPerWave) return false;
+  // every workgroup must own at least one gate/up pair (the epoch hand-over
+  // relies on workgroup 0 consuming a value from each of them)
+  if (units * rmoe::kFusedI < waves) return false;
+  *grid = g;
+  return true;
+}
+
+rmoe::FusedLayer fused_layer(const rmoe_layer* L) {
+  rmoe::FusedLayer f{};
+  f.router_w = L->router_w;
+  f.sgate_w = L->shared_gate_up.w ? L->shared_gate_w : nullptr;
+  f.gu = qw(L->gate_up);
+  f.dn = qw(L->down);
+  f.sgu = qw(L->shared_gate_up);
+  f.sdn = qw(L->shared_down);
+  return f;
+}
+
+rmoe::FusedArgs fused_args(const rmoe_layer* L, const uint16_t* x, uint16_t* out, void* ws) {
+  const Layout l = layout(1, L->experts, L->top_k, L->inter);
+  rmoe::FusedArgs f{};
+  f.n_layers = 1;
+  f.E = L->experts;
+  f.K = L->top_k;
+  f.norm = L->norm_topk_prob != 0;
+  f.has_shared = L->shared_gate_up.w != nullptr;
+  f.layer0 = fused_layer(L);
+  f.table = nullptr;
+  f.x = x;
+  f.out = out;
+  f.scratch = reinterpret_cast<rmoe::FusedScratch*>(static_cast<char*>(ws) + l.fused);
+  return f;
 }
 
 }  // namespace
@@ -296,13 +345,25 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
     return fail(RMOE_EINVAL, "out must not alias x");
   const size_t need = layout(tokens, L->experts, L->top_k, L->inter).total;
   if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bits = L->gate_up.bits;
+  int grid = 0;
+  if (tokens == 1 && fused_eligible(L, &grid)) {
+    rmoe::FusedArgs f = fused_args(L, x, out, ws);
+    f.n_layers = 1;
+    f.residual_mode = residual == nullptr ? 0 : (residual == x ? 1 : 2);
+    f.residual = residual;
+    f.idx_out = indices_out;
+    f.scores_out = scores_out;
+    const hipError_t e = rmoe::launch_fused_decode(f, bits, grid, s);
+    if (e != hipSuccess) return hip_fail(e, "fused decode launch");
+    return ok();
+  }
   rmoe::DecodeArgs a = decode_args(L, x, tokens, ws);
   a.out = out;
   a.residual = residual;
   a.idx_out = indices_out;
   a.scores_out = scores_out;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int bits = L->gate_up.bits;
   hipError_t e = rmoe::launch_router(a, s);
   if (e != hipSuccess) return hip_fail(e, "router launch");
   e = rmoe::launch_gate_up(a, bits, s);
@@ -422,6 +483,65 @@ int rmoe_dequantize(const rmoe_qweight* w, int64_t row_begin, int64_t rows,
                               out_bf16, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "dequantize launch");
   return ok();
+}
+
+size_t rmoe_chain_table_bytes(int32_t n_layers) {
+  return n_layers > 0 ? (size_t)n_layers * sizeof(rmoe::FusedLayer) : 0;
+}
+
+int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers, void* host_table) {
+  int rc;
+  if (!layers || !host_table) return fail(RMOE_ENULL, "layers and host_table are required");
+  if (n_layers < 1) return fail(RMOE_EINVAL, "n_layers must be >= 1");
+  int grid = 0;
+  for (int i = 0; i < n_layers; ++i) {
+    if ((rc = check_layer(&layers[i]))) return rc;
+    const rmoe_layer& a = layers[0];
+    const rmoe_layer& b = layers[i];
+    if (b.hidden != a.hidden || b.inter != a.inter || b.experts != a.experts ||
+        b.top_k != a.top_k || b.norm_topk_prob != a.norm_topk_prob ||
+        b.gate_up.bits != a.gate_up.bits ||
+        (b.shared_gate_up.w == nullptr) != (a.shared_gate_up.w == nullptr) ||
+        (b.shared_gate_w == nullptr) != (a.shared_gate_w == nullptr))
+      return fail(RMOE_EINVAL, "layer %d differs in shape or format from layer 0", i);
+    if (!fused_eligible(&b, &grid))
+      return fail(RMOE_EINVAL,
+                  "chained decode needs hidden %d, inter %d, top_k + shared <= %d, "
+                  "experts <= %d and one resident workgroup per CU",
+                  rmoe::kFusedH, rmoe::kFusedI, rmoe::kMaxFusedUnits, rmoe::kFusedMaxExperts);
+    static_cast<rmoe::FusedLayer*>(host_table)[i] = fused_layer(&b);
+  }
+  return ok();
+}
+
+int rmoe_moe_chain(const rmoe_layer* layer0, const void* device_table, int32_t n_layers,
+                   const uint16_t* x, uint16_t* out, void* ws, size_t ws_bytes,
+                   void* stream) {
+  int rc;
+  if ((rc = check_layer(layer0))) return rc;
+  if (!device_table || !x || !out) return fail(RMOE_ENULL, "table, x and out are required");
+  if (n_layers < 1) return fail(RMOE_EINVAL, "n_layers must be >= 1");
+  if (!aligned(x, 16) || !aligned(device_table, 8))
+    return fail(RMOE_EALIGN, "x must be 16-byte and the table 8-byte aligned");
+  if (static_cast<const void*>(out) == static_cast<const void*>(x))
+    return fail(RMOE_EINVAL, "out must not alias x");
+  int grid = 0;
+  if (!fused_eligible(layer0, &grid))
+    return fail(RMOE_EINVAL, "layer shape is not supported by the chained decode kernel");
+  const size_t need = layout(1, layer0->experts, layer0->top_k, layer0->inter).total;
+  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  rmoe::FusedArgs f = fused_args(layer0, x, out, ws);
+  f.n_layers = n_layers;
+  f.table = static_cast<const rmoe::FusedLayer*>(device_table);
+  f.residual_mode = 1;
+  const hipError_t e = rmoe::launch_fused_decode(f, layer0->gate_up.bits, grid,
+                                                 static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "chained decode launch");
+  return ok();
+}
+
+size_t rmoe_workspace_status_offset(void) {
+  return layout(0, 1, 1, 0).fused + offsetof(rmoe::FusedScratch, err);
 }
 
 int rmoe_stream_read(const void* buffer, size_t bytes, uint32_t* partials,

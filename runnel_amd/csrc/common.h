@@ -31,18 +31,60 @@ __device__ __forceinline__ float round_bf16(float v) {
 }
 
 // ------------------------------------------------------- wave reductions
-// Butterfly p <- p + p[lane ^ d], d = 32..1: every lane ends with the same
-// value, and the order of additions is fixed (the router relies on it).
+// Butterfly p <- p + p[lane ^ d], d = 1, 2, 4, 8, 16, 32: every lane ends
+// with the same value, and the order of additions is fixed (the router's
+// bit-exact contract relies on it).  Reference form; wave_sum below is the
+// fast equivalent.
 __device__ __forceinline__ float wave_sum_butterfly(float v) {
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  for (int d = 1; d <= 32; d <<= 1) v += __shfl_xor(v, d, kWave);
   return v;
 }
 // Sum within aligned segments of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float segment_sum(float v, int width) {
-  for (int d = width >> 1; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  for (int d = 1; d < width; d <<= 1) v += __shfl_xor(v, d, kWave);
   return v;
 }
+// The same butterfly with cheap cross-lane operations.  After each level
+// every lane of a block holds the same value, so adding the mirrored
+// partner (DPP row_half_mirror / row_mirror) or the swizzled one gives the
+// exact value the xor partner would: the results equal wave_sum_butterfly
+// bit for bit.
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
+  int r;
+  switch (ctrl) {  // the control must be a compile-time constant
+    case 0xB1: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false); break;
+    case 0x4E: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false); break;
+    case 0x141: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false); break;
+  }
+  return __int_as_float(r);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f(v, 0xB1);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp_f(v, 0x4E);   // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp_f(v, 0x141);  // row_half_mirror: the other quad of the 8
+  v += dpp_f(v, 0x140);  // row_mirror: the other 8 of the row
+  // ds_swizzle bit mode, xor 16 within each 32 lanes
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+// Sum within aligned segments of `width` lanes (a power of two, 1..64) with
+// the same butterfly order; every lane of a segment gets the segment sum.
+__device__ __forceinline__ float segment_sum_fast(float v, int width) {
+  if (width >= 2) v += dpp_f(v, 0xB1);
+  if (width >= 4) v += dpp_f(v, 0x4E);
+  if (width >= 8) v += dpp_f(v, 0x141);
+  if (width >= 16) v += dpp_f(v, 0x140);
+  if (width >= 32)
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  if (width >= 64)
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  return v;
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
@@ -50,6 +92,50 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = o > v ? o : v;
   }
   return v;
+}
+
+// ------------------------------------------------------------ top-k keys
+// Keys are unique and nonzero: (bf16 order key << 16) | (0xFFFF - index), so
+// "larger key" = larger logit, then lower index.  Selects the k largest of
+// the P keys per lane (absent keys are 0) without serial max rounds: a
+// 32-step ballot search finds the k-th largest key, the selected keys are
+// compacted into `lds[0..k)` and ranked.  Must be called by a whole wave;
+// returns, in lane j < k, the key of rank j (descending).
+template <int P>
+__device__ __forceinline__ uint32_t wave_topk(const uint32_t (&keys)[P], int k,
+                                              uint32_t* lds) {
+  const int lane = threadIdx.x & 63;
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) cnt += __popcll(__ballot(keys[i] >= cand));
+    if (cnt >= k) thr = cand;
+  }
+  int before = 0;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const bool sel = keys[i] >= thr && keys[i] != 0u;
+    const unsigned long long m = __ballot(sel);
+    if (sel) lds[before + __popcll(m & lt)] = keys[i];
+    before += __popcll(m);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  uint32_t mine = 0;
+  int rank = 0;
+  if (lane < k) {
+    mine = lds[lane];
+    for (int j = 0; j < k; ++j) rank += lds[j] > mine ? 1 : 0;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  if (lane < k) lds[64 + rank] = mine;
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  return lane < k ? lds[64 + lane] : 0u;
 }
 
 // ------------------------------------------------------- packed dot chunks
@@ -121,17 +207,22 @@ __device__ __forceinline__ uint32_t bf16_from_order_key(uint32_t k) {
   return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu);
 }
 
-// Agent-scope release / acquire around workgroup hand-offs (the L2 of each
-// XCD is private, so plain stores need the release before a counter bump and
-// readers need the acquire after observing it).
-__device__ __forceinline__ void fence_release() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+// Cross-workgroup hand-off without whole-cache maintenance.  Each XCD has a
+// private L2, and an agent-scope release/acquire fence writes back or
+// invalidates that entire L2 (microseconds per wave).  Instead, the few
+// values handed over are stored and loaded with agent-scope atomics, which
+// are coherent on their own (write-through / bypassing stale lines); the
+// producer waits for its stores to be acknowledged before bumping the
+// counter.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void fence_acquire() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t atomic_add_acq_rel(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ uint32_t atomic_add_agent(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace rmoe

@@ -18,6 +18,7 @@
 namespace rmoe {
 
 // ------------------------------------------------------------------ router
+template <int P>
 __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   const int t = blockIdx.y;
   const int wave = threadIdx.x >> 6;
@@ -32,72 +33,72 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
         row < p.E ? p.router_w + (size_t)row * p.H : p.sgate_w;
     float acc = 0.0f;
     const int chunks = p.H >> 3;
-    for (int c = lane; c < chunks; c += 64) {
-      const uint4 xv = load16(xt + c * 8);
-      const uint4 wv = load16_stream(wr + c * 8);
-      acc = fmaf(bf16_lo(xv.x), bf16_lo(wv.x), acc);
-      acc = fmaf(bf16_hi(xv.x), bf16_hi(wv.x), acc);
-      acc = fmaf(bf16_lo(xv.y), bf16_lo(wv.y), acc);
-      acc = fmaf(bf16_hi(xv.y), bf16_hi(wv.y), acc);
-      acc = fmaf(bf16_lo(xv.z), bf16_lo(wv.z), acc);
-      acc = fmaf(bf16_hi(xv.z), bf16_hi(wv.z), acc);
-      acc = fmaf(bf16_lo(xv.w), bf16_lo(wv.w), acc);
-      acc = fmaf(bf16_hi(xv.w), bf16_hi(wv.w), acc);
+    // All loads of the row are issued before the first multiply (one memory
+    // round trip); the accumulation order is still chunk by chunk.
+    for (int c0 = lane; c0 < chunks; c0 += 64 * kRouterBatch) {
+      uint4 xv[kRouterBatch], wv[kRouterBatch];
+#pragma unroll
+      for (int i = 0; i < kRouterBatch; ++i) {
+        const int c = c0 + 64 * i;
+        xv[i] = wv[i] = make_uint4(0, 0, 0, 0);
+        if (c < chunks) {
+          xv[i] = load16(xt + c * 8);
+          wv[i] = load16_stream(wr + c * 8);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kRouterBatch; ++i) {
+        if (c0 + 64 * i < chunks) {
+          acc = fmaf(bf16_lo(xv[i].x), bf16_lo(wv[i].x), acc);
+          acc = fmaf(bf16_hi(xv[i].x), bf16_hi(wv[i].x), acc);
+          acc = fmaf(bf16_lo(xv[i].y), bf16_lo(wv[i].y), acc);
+          acc = fmaf(bf16_hi(xv[i].y), bf16_hi(wv[i].y), acc);
+          acc = fmaf(bf16_lo(xv[i].z), bf16_lo(wv[i].z), acc);
+          acc = fmaf(bf16_hi(xv[i].z), bf16_hi(wv[i].z), acc);
+          acc = fmaf(bf16_lo(xv[i].w), bf16_lo(wv[i].w), acc);
+          acc = fmaf(bf16_hi(xv[i].w), bf16_hi(wv[i].w), acc);
+        }
+      }
     }
-    acc = wave_sum_butterfly(acc);
-    if (lane == 0) lg[row] = acc;
+    acc = wave_sum(acc);
+    if (lane == 0) store_coherent(lg + row, acc);
   }
 
   // Last workgroup of this token ranks the logits.
   __shared__ uint32_t s_last;
-  fence_release();
+  __shared__ uint32_t s_topk[128];
+  wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = atomic_add_acq_rel(&p.ctr[t], 1u);
+    const uint32_t prev = atomic_add_agent(&p.ctr[t], 1u);
     s_last = (prev == gridDim.x - 1) ? 1u : 0u;
   }
   __syncthreads();
   if (s_last == 0u || wave != 0) return;
-  fence_acquire();
 
-  constexpr int kMaxPer = kMaxExperts / 64;
-  uint32_t keys[kMaxPer];
-  uint32_t lbits[kMaxPer];
+  uint32_t keys[P];
+  float lv[P];
 #pragma unroll
-  for (int i = 0; i < kMaxPer; ++i) {
+  for (int i = 0; i < P; ++i) {
     const int e = lane + 64 * i;
-    lbits[i] = 0;
+    lv[i] = 0.0f;
     keys[i] = 0;
     if (e < p.E) {
-      const uint32_t b = f32_to_bf16(lg[e]);
-      lbits[i] = b;
+      const uint32_t b = f32_to_bf16(load_coherent(lg + e));
+      lv[i] = bf16_to_f32(b);
       keys[i] = (bf16_order_key(b) << 16) | (0xFFFFu - (uint32_t)e);
     }
   }
-  int my_sel = -1;
-  float my_logit = 0.0f;
-  uint32_t first = 0;
-  for (int j = 0; j < p.K; ++j) {
-    uint32_t mine = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) mine = keys[i] > mine ? keys[i] : mine;
-    const uint32_t best = wave_max_u32(mine);
-    if (j == 0) first = best;
-    const int e = (int)(0xFFFFu - (best & 0xFFFFu));
-#pragma unroll
-    for (int i = 0; i < kMaxPer; ++i)
-      if (lane + 64 * i == e) keys[i] = 0;
-    if (lane == j) {
-      my_sel = e;
-      my_logit = bf16_to_f32(bf16_from_order_key(best >> 16));
-    }
-  }
-  const float m = bf16_to_f32(bf16_from_order_key(first >> 16));
+  const uint32_t my_key = wave_topk<P>(keys, p.K, s_topk);
+  const uint32_t top_key = __builtin_amdgcn_readfirstlane(my_key);
+  const float m = bf16_to_f32(bf16_from_order_key(top_key >> 16));
   float z = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kMaxPer; ++i)
-    if (lane + 64 * i < p.E) z += __expf(bf16_to_f32(lbits[i]) - m);
-  z = wave_sum_butterfly(z);
+  for (int i = 0; i < P; ++i)
+    if (lane + 64 * i < p.E) z += __expf(lv[i] - m);
+  z = wave_sum(z);
+  const int my_sel = (int)(0xFFFFu - (my_key & 0xFFFFu));
+  const float my_logit = bf16_to_f32(bf16_from_order_key(my_key >> 16));
   float pb = 0.0f;
   if (lane < p.K) pb = round_bf16(__expf(my_logit - m) / z);
   float total = 0.0f;
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   }
   if (lane == 0) {
     float sg = 1.0f;
-    if (has_sg) sg = round_bf16(sigmoid(round_bf16(lg[p.E])));
+    if (has_sg) sg = round_bf16(sigmoid(round_bf16(load_coherent(lg + p.E))));
     p.scores[t * (p.K + 1) + p.K] = sg;
     __hip_atomic_store(&p.ctr[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -213,8 +214,8 @@ __global__ __launch_bounds__(256) void gate_up_kernel(const DecodeArgs p,
       au += su[pp][i] * qdot_chunk<BITS>(wu[pp][i], xv[i]) + bu[pp][i] * xs[i];
       ag += sg[pp][i] * qdot_chunk<BITS>(wg[pp][i], xv[i]) + bg[pp][i] * xs[i];
     }
-    au = wave_sum_butterfly(au);
-    ag = wave_sum_butterfly(ag);
+    au = wave_sum(au);
+    ag = wave_sum(ag);
     if (lane == 0) {
       const float up = round_bf16(au);
       const float gate = round_bf16(ag);
@@ -239,12 +240,41 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
   const int I = p.I;
   const int H = p.H;
   const float* act_t = p.act + (size_t)t * U1 * I;
-  for (int i = threadIdx.x; i < units * I; i += blockDim.x) s_act[i] = act_t[i];
+  const int CHR = I / VPC;  // chunks per row: power of two <= 64
+  // Transposed staging: value v of chunk ch of unit u at u*I + v*CHR + ch,
+  // so the lanes of a row (consecutive ch) read consecutive banks.
+  {
+    // 16-byte loads, all issued before the LDS stores (one round trip).
+    const int n4 = units * I / 4;
+    const float4* src4 = reinterpret_cast<const float4*>(act_t);
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * kStageBatch) {
+      float4 v[kStageBatch];
+#pragma unroll
+      for (int b = 0; b < kStageBatch; ++b) {
+        const int i = i0 + 256 * b;
+        if (i < n4) v[b] = src4[i];
+      }
+#pragma unroll
+      for (int b = 0; b < kStageBatch; ++b) {
+        const int i = i0 + 256 * b;
+        if (i < n4) {
+          const float vals[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int e = 4 * i + q;
+            const int u = e / I;
+            const int k = e - u * I;
+            const int c = k / VPC;
+            s_act[u * I + (k - c * VPC) * CHR + c] = vals[q];
+          }
+        }
+      }
+    }
+  }
   __syncthreads();
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int CHR = I / VPC;  // chunks per row: power of two <= 64
   const int RPL = 64 / CHR;
   const int r = lane / CHR;
   const int ch = lane - r * CHR;
@@ -281,14 +311,14 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
       if (u >= units) continue;  // wave-uniform
       float a[VPC];
       float asum = 0.0f;
-      const float* src = s_act + u * I + ch * VPC;
+      const float* src = s_act + u * I + ch;
 #pragma unroll
       for (int v = 0; v < VPC; ++v) {
-        a[v] = src[v];
+        a[v] = src[v * CHR];
         asum += a[v];
       }
       float y = sv[b] * qdot_chunk<BITS>(wv[b], a) + bv[b] * asum;
-      y = round_bf16(segment_sum(y, CHR));
+      y = round_bf16(segment_sum_fast(y, CHR));
       if constexpr (COMBINE) {
         acc += p.scores[t * (p.K + 1) + u] * y;
       } else {
@@ -381,7 +411,10 @@ __global__ __launch_bounds__(256) void qmv_kernel(const QmvArgs p,
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
   const int rows = a.E + (a.sgate_w ? 1 : 0);
   dim3 grid((rows + 3) / 4, a.T);
-  hipLaunchKernelGGL(router_kernel, grid, dim3(256), 0, s, a);
+  if (a.E <= 256)
+    hipLaunchKernelGGL(router_kernel<4>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(router_kernel<kMaxExperts / 64>, grid, dim3(256), 0, s, a);
   RMOE_CHECK_LAUNCH();
   return hipSuccess;
 }

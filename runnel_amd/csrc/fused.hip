@@ -1,0 +1,633 @@
+// Single-launch batch-1 decode of one or more MoE layers (gfx950).
+//
+// One workgroup of 8 waves per CU, launched cooperatively so every
+// workgroup is resident.  Per layer:
+//
+//   R  router rows, one per workgroup (the fixed-order dot of the router
+//      contract); the row weights are loaded before x is even staged
+//   K  every workgroup ranks all logits itself: 4 keys per lane sorted
+//      locally, then top_k rounds of a DPP wave maximum
+//   G  gate/up pairs: every wave issues the loads of all its pairs and of
+//      its down row of every unit at once (about 110 KB per CU in flight),
+//      computes SwiGLU
+//   D  the down row of every unit from registers, weighted combine, gated
+//      shared expert, residual, bf16 out
+//
+// The routing-independent loads of the shared expert are issued first.
+//
+// Values handed between workgroups (logits, activations, a chained layer's
+// output) are tagged words, (bf16 value << 16) | (phase & 0xFFFF), written
+// and read with agent-scope atomics.  A consumer polls the data itself until
+// every tag it needs shows the current phase: no separate flag round trip,
+// no same-address atomics (which serialise across CUs), no resets.  The
+// phase base comes from an epoch word read at start; workgroup 0 advances
+// it once per launch after it has consumed a tagged value from every
+// workgroup (every workgroup owns at least one gate/up pair, which the
+// host checks), so every workgroup has read the old epoch by then.  Every
+// wait is bounded: on timeout the kernel sets a status word and still runs
+// to completion.
+#include "common.h"
+#include "kernels.h"
+
+namespace rmoe {
+
+namespace {
+
+constexpr int kThreads = kFusedThreads;
+constexpr int kWaves = kThreads / 64;
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_coherent_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t tagged(uint32_t bf16_bits, uint32_t tag) {
+  return (bf16_bits << 16) | (tag & 0xFFFFu);
+}
+__device__ __forceinline__ bool tag_ok(uint32_t word, uint32_t tag) {
+  return (word & 0xFFFFu) == (tag & 0xFFFFu);
+}
+
+// Wave maximum of unsigned keys with the DPP pattern of wave_sum; the
+// result is uniform.
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v, int ctrl) {
+  switch (ctrl) {
+    case 0xB1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    case 0x4E: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    case 0x141: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);
+  }
+}
+__device__ __forceinline__ uint32_t wave_max_fast(uint32_t v) {
+  v = max(v, dpp_u(v, 0xB1));
+  v = max(v, dpp_u(v, 0x4E));
+  v = max(v, dpp_u(v, 0x141));
+  v = max(v, dpp_u(v, 0x140));
+  v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  return a > b ? a : b;
+}
+__device__ __forceinline__ void cswap_desc(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = a > b ? a : b;
+  const uint32_t lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+
+template <int BITS>
+struct Shape {
+  static constexpr int H = kFusedH;
+  static constexpr int I = kFusedI;
+  static constexpr int GU_CPL = H * BITS / 8 / (64 * 16);  // 16-B chunks per lane: 2 | 1
+  static constexpr int VPC = BITS == 8 ? 16 : 32;          // values per chunk
+  static constexpr int GU_WPR = H * BITS / 32;             // words per gate/up row
+  static constexpr int DN_WPL = 8 * BITS / 32;             // down words per lane: 2 | 1
+  static constexpr int DN_WPR = I * BITS / 32;             // words per down row
+};
+
+}  // namespace
+
+// Loads of one gate/up pair (up row c and gate row c + I of one unit): the
+// packed chunks of this lane, and one 4-byte word per lane that together
+// cover every scale and bias of both rows (lanes 0-15: up scales, 16-31:
+// gate scales, 32-47: up biases, 48-63: gate biases; 16 words = 32 bf16 =
+// one row's groups).  A lane's own group values come from `param_of`.
+template <int CPL>
+struct PairRegs {
+  uint4 wu[CPL], wg[CPL];
+  uint32_t pw;
+};
+
+template <int BITS, int CPL>
+__device__ __forceinline__ void load_pair_params(PairRegs<CPL>& r, const QW& bank,
+                                                 size_t up_row, int lane) {
+  using S = Shape<BITS>;
+  static_assert(S::H / 64 == 32, "16 words of bf16 per row");
+  const size_t row = up_row + ((lane >> 4) & 1) * S::I;
+  const uint16_t* base = (lane < 32 ? bank.s : bank.b) + row * (S::H / 64);
+  r.pw = reinterpret_cast<const uint32_t*>(base)[lane & 15];
+}
+
+template <int BITS, int CPL>
+__device__ __forceinline__ void load_pair_words(PairRegs<CPL>& r, const QW& bank,
+                                                size_t up_row, int lane) {
+  using S = Shape<BITS>;
+  const size_t gate_row = up_row + S::I;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = lane + 64 * i;
+    r.wu[i] = load16_stream(bank.w + up_row * S::GU_WPR + ch * 4);
+    r.wg[i] = load16_stream(bank.w + gate_row * S::GU_WPR + ch * 4);
+  }
+}
+
+// bf16 value of group g held in the word array spread over lanes
+// [first, first + 16): word g / 2, half g % 2.
+__device__ __forceinline__ float param_of(uint32_t word, int first, int g) {
+  const uint32_t w = (uint32_t)__shfl((int)word, first + (g >> 1), 64);
+  return __uint_as_float((g & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+
+// Down row h of one unit: lane l holds values [8l, 8l + 8).  Scales and
+// biases of up to 8 units' rows come in one word per lane (lane 8u + j:
+// unit u, j < 4 scale words, j >= 4 bias words).
+template <int WPL>
+struct DownRegs {
+  uint32_t w[WPL];
+};
+
+template <int BITS>
+__device__ __forceinline__ uint32_t load_down_param_word(const QW& bank, size_t row, int j) {
+  using S = Shape<BITS>;
+  static_assert(S::I / 64 == 8, "4 words of bf16 per down row");
+  const uint16_t* base = (j < 4 ? bank.s : bank.b) + row * (S::I / 64);
+  return reinterpret_cast<const uint32_t*>(base)[j & 3];
+}
+
+template <int BITS>
+__device__ __forceinline__ void load_down_words(DownRegs<Shape<BITS>::DN_WPL>& r,
+                                                const QW& bank, size_t row, int lane) {
+  using S = Shape<BITS>;
+  const uint32_t* src = bank.w + row * S::DN_WPR + lane * S::DN_WPL;
+  if constexpr (S::DN_WPL == 2) {
+    const uint2 v = *reinterpret_cast<const uint2*>(src);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else {
+    r.w[0] = src[0];
+  }
+}
+
+// Keep the compiler from moving loads or their uses across this point, so
+// that every load of a batch is issued before the first wait on any of them.
+__device__ __forceinline__ void issue_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Routing-independent loads of one layer for this wave: its router row and,
+// for the shared expert (unit K), its gate/up pairs and its down row.  For
+// a chained layer they are issued while the previous layer finishes.
+template <int BITS, int CPL, int NP, int RC>
+__device__ __forceinline__ void issue_prologue(const FusedLayer& L, int row, int n_rows, int E,
+                                               bool has_shared, int K, int gwave, int n_waves,
+                                               int n_pairs, int h, int lane, uint4 (&rw)[RC],
+                                               PairRegs<CPL> (&pr)[NP],
+                                               DownRegs<Shape<BITS>::DN_WPL>& drs,
+                                               uint32_t& dpws) {
+  using S = Shape<BITS>;
+  constexpr int I = S::I;
+  constexpr int H = S::H;
+  if (row < n_rows) {
+    const uint16_t* wr = row < E ? L.router_w + (size_t)row * H : L.sgate_w;
+#pragma unroll
+    for (int i = 0; i < RC; ++i) rw[i] = load16_stream(wr + (lane + 64 * i) * 8);
+  }
+  if (has_shared) {
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const int q = gwave + pp * n_waves;
+      if (q < n_pairs && q / I == K) load_pair_params<BITS, CPL>(pr[pp], L.sgu, q - K * I, lane);
+    }
+    if (h < H && lane < 8) dpws = load_down_param_word<BITS>(L.sdn, h, lane);
+    issue_fence();
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const int q = gwave + pp * n_waves;
+      if (q < n_pairs && q / I == K) load_pair_words<BITS, CPL>(pr[pp], L.sgu, q - K * I, lane);
+    }
+    if (h < H) load_down_words<BITS>(drs, L.sdn, h, lane);
+  }
+  issue_fence();
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs p) {
+  using S = Shape<BITS>;
+  constexpr int H = S::H;
+  constexpr int I = S::I;
+  constexpr int VPC = S::VPC;
+  constexpr int CPL = S::GU_CPL;
+  constexpr int NP = kMaxFusedPairsPerWave;
+  constexpr int NU = kMaxFusedUnits;
+  constexpr int kStageX = H / kThreads;                     // 4
+  constexpr int kStageAct = NU * I / kThreads;              // 9
+  constexpr int kPer = kFusedMaxExperts / 64;               // keys per lane (4)
+  constexpr int RC = H / 8 / 64;                            // router chunks per lane
+  static_assert(kPer == 4, "the local sort network below is for 4 keys per lane");
+  const int G = gridDim.x;
+  const int wg = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane0 = threadIdx.x & 63;
+  const int gwave = wg * kWaves + wave;
+  const int n_waves = G * kWaves;
+  const int K = p.K;
+  const int E = p.E;
+  const int U = K + p.has_shared;
+  const int n_pairs = U * I;
+  const int h = gwave;            // one down row per wave (n_waves >= H is checked)
+  const int row = wg + G * wave;  // router row of this wave, if any
+  FusedScratch* sc = p.scratch;
+
+  __shared__ float s_x[H];
+  __shared__ float s_act[NU * I];
+  __shared__ float s_asum[NU * 64];
+  __shared__ int s_idx[NU];
+  __shared__ float s_coef[NU];
+  __shared__ uint32_t s_base;
+
+  // Layer 0's input first (it gates the router), then the prologue loads.
+  uint32_t xin[kStageX];
+#pragma unroll
+  for (int j = 0; j < kStageX; ++j) xin[j] = (uint32_t)p.x[threadIdx.x + j * kThreads] << 16;
+  if (threadIdx.x == 0) s_base = load_coherent_u32(&sc->epoch);
+
+  PairRegs<CPL> pr[NP];
+  DownRegs<S::DN_WPL> dr[NU];      // slot NU-1: the shared unit
+  DownRegs<S::DN_WPL> dr_next;     // the next layer's shared down row
+  uint32_t dpw0 = 0, dpw1 = 0, dpw1_next = 0;
+  uint4 rw[RC];
+  {
+    const FusedLayer L0 = p.table ? p.table[0] : p.layer0;
+    const int n_rows0 = E + ((p.has_shared && L0.sgate_w) ? 1 : 0);
+    issue_prologue<BITS, CPL, NP, RC>(L0, row, n_rows0, E, p.has_shared, K, gwave, n_waves,
+                                      n_pairs, h, lane0, rw, pr, dr[NU - 1], dpw1);
+  }
+  __syncthreads();
+  const uint32_t base = s_base;
+  uint32_t phase = 0;
+  bool timed_out = false;
+
+  for (int layer = 0; layer < p.n_layers; ++layer) {
+    // An opaque per-iteration copy of the lane index: stops the compiler from
+    // hoisting every per-lane address of the layer out of the loop (which
+    // would keep them live across all layers and spill them).
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const FusedLayer L = p.table ? p.table[layer] : p.layer0;
+    const bool first = layer == 0;
+    const bool last = layer == p.n_layers - 1;
+    const uint32_t tag_logit = base + phase + 1;
+    const uint32_t tag_act = base + phase + 2;
+    const uint32_t tag_x = base + phase + 3;  // used when a next layer reads x
+    phase += last ? 2 : 3;
+    const bool sg_row = p.has_shared && L.sgate_w;
+    const int n_rows = E + (sg_row ? 1 : 0);
+
+    // ---- x (bf16 -> fp32 in LDS).  A chained layer polls the previous
+    // layer's tagged output.
+    {
+      if (!first) {
+        const uint32_t* src = sc->xs[(layer - 1) & 1];
+        const uint32_t want = tag_logit - 1;  // the previous layer's tag_x
+        for (int spin = 0;; ++spin) {
+          bool ok = true;
+#pragma unroll
+          for (int j = 0; j < kStageX; ++j) {
+            xin[j] = load_coherent_u32(src + threadIdx.x + j * kThreads);
+            ok &= tag_ok(xin[j], want);
+          }
+          if (ok) break;
+          if (spin >= kSpinLimit) { timed_out = true; break; }
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kStageX; ++j)
+        s_x[threadIdx.x + j * kThreads] = __uint_as_float(xin[j] & 0xFFFF0000u);
+    }
+    __syncthreads();
+
+    // ---- R: this wave's router row.
+    if (row < n_rows) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < RC; ++i) {
+        const float* xv = s_x + (lane + 64 * i) * 8;
+        acc = fmaf(xv[0], bf16_lo(rw[i].x), acc);
+        acc = fmaf(xv[1], bf16_hi(rw[i].x), acc);
+        acc = fmaf(xv[2], bf16_lo(rw[i].y), acc);
+        acc = fmaf(xv[3], bf16_hi(rw[i].y), acc);
+        acc = fmaf(xv[4], bf16_lo(rw[i].z), acc);
+        acc = fmaf(xv[5], bf16_hi(rw[i].z), acc);
+        acc = fmaf(xv[6], bf16_lo(rw[i].w), acc);
+        acc = fmaf(xv[7], bf16_hi(rw[i].w), acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) store_coherent_u32(sc->logits + row, tagged(f32_to_bf16(acc), tag_logit));
+    }
+
+    // ---- K: poll all logits (wave 0), rank them, publish in LDS.
+    if (wave == 0) {
+      uint32_t w[kPer];
+      uint32_t wsg = 0;
+      for (int spin = 0;; ++spin) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const int e = lane + 64 * i;
+          w[i] = e < E ? load_coherent_u32(sc->logits + e) : 0u;
+          ok &= e >= E || tag_ok(w[i], tag_logit);
+        }
+        if (sg_row && lane == 0) {
+          wsg = load_coherent_u32(sc->logits + E);
+          ok &= tag_ok(wsg, tag_logit);
+        }
+        if (__all(ok)) break;
+        if (spin >= kSpinLimit) { timed_out = true; break; }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      uint32_t k[kPer];
+      float lv[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int e = lane + 64 * i;
+        const uint32_t b = w[i] >> 16;
+        lv[i] = bf16_to_f32(b);
+        k[i] = e < E ? ((bf16_order_key(b) << 16) | (0xFFFFu - (uint32_t)e)) : 0u;
+      }
+      // local sort (descending), then top_k rounds of a wave maximum over
+      // the lanes' current heads
+      cswap_desc(k[0], k[1]);
+      cswap_desc(k[2], k[3]);
+      cswap_desc(k[0], k[2]);
+      cswap_desc(k[1], k[3]);
+      cswap_desc(k[1], k[2]);
+      uint32_t sel[NU - 1];
+#pragma unroll
+      for (int j = 0; j < NU - 1; ++j) {
+        sel[j] = 0;
+        if (j < K) {
+          const uint32_t best = wave_max_fast(k[0]);
+          sel[j] = best;
+          if (k[0] == best) {
+            k[0] = k[1];
+            k[1] = k[2];
+            k[2] = k[3];
+            k[3] = 0;
+          }
+        }
+      }
+      const float m = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
+      float z = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        if (lane + 64 * i < E) z += __expf(lv[i] - m);
+      z = wave_sum(z);
+      // slot j is handled by lane j
+      uint32_t my = 0;
+#pragma unroll
+      for (int j = 0; j < NU - 1; ++j)
+        if (lane == j) my = sel[j];
+      const float pb =
+          lane < K ? round_bf16(__expf(bf16_to_f32(bf16_from_order_key(my >> 16)) - m) / z) : 0.0f;
+      float total = 0.0f;  // slot order, as the oracle sums
+#pragma unroll
+      for (int j = 0; j < NU - 1; ++j)
+        if (j < K) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
+      if (lane < K) {
+        const int e = (int)(0xFFFFu - (my & 0xFFFFu));
+        const float score = p.norm ? round_bf16(pb / total) : pb;
+        s_idx[lane] = e;
+        s_coef[lane] = score;
+        if (wg == 0 && last && p.idx_out) {
+          p.idx_out[lane] = e;
+          p.scores_out[lane] = score;
+        }
+      }
+      if (lane == 0 && p.has_shared) {
+        s_idx[K] = 0;
+        s_coef[K] = sg_row ? round_bf16(sigmoid(bf16_to_f32(wsg >> 16))) : 1.0f;
+      }
+    }
+    __syncthreads();
+
+    // ---- routed loads: parameters first, then packed words.
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const int q = gwave + pp * n_waves;
+      const int u = q / I;
+      if (q < n_pairs && u < K)
+        load_pair_params<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
+    }
+    if (h < H && (lane >> 3) < K)
+      dpw0 = load_down_param_word<BITS>(L.dn, (size_t)s_idx[lane >> 3] * H + h, lane & 7);
+    issue_fence();
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const int q = gwave + pp * n_waves;
+      const int u = q / I;
+      if (q < n_pairs && u < K)
+        load_pair_words<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
+    }
+#pragma unroll
+    for (int u = 0; u < NU - 1; ++u)
+      if (u < K && h < H) load_down_words<BITS>(dr[u], L.dn, (size_t)s_idx[u] * H + h, lane);
+    issue_fence();
+
+    // ---- G: gate/up + SwiGLU of this wave's pairs -> tagged act words.
+    // x of this lane's chunks is the same for every pair.
+    float xv[CPL][VPC];
+    float xs[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = lane + 64 * i;
+      xs[i] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < VPC; v += 4) {
+        const float4 f = *reinterpret_cast<const float4*>(s_x + ch * VPC + v);
+        xv[i][v] = f.x;
+        xv[i][v + 1] = f.y;
+        xv[i][v + 2] = f.z;
+        xv[i][v + 3] = f.w;
+      }
+#pragma unroll
+      for (int v = 0; v < VPC; ++v) xs[i] += xv[i][v];
+    }
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const int q = gwave + pp * n_waves;
+      if (q >= n_pairs) continue;  // wave-uniform
+      float au = 0.0f, ag = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int ch = lane + 64 * i;
+        const int g = (ch * VPC) >> 6;
+        au += param_of(pr[pp].pw, 0, g) * qdot_chunk<BITS>(pr[pp].wu[i], xv[i]) +
+              param_of(pr[pp].pw, 32, g) * xs[i];
+        ag += param_of(pr[pp].pw, 16, g) * qdot_chunk<BITS>(pr[pp].wg[i], xv[i]) +
+              param_of(pr[pp].pw, 48, g) * xs[i];
+      }
+      au = wave_sum(au);
+      ag = wave_sum(ag);
+      if (lane == 0) {
+        const float up = round_bf16(au);
+        const float gate = round_bf16(ag);
+        store_coherent_u32(sc->act + q, tagged(f32_to_bf16(silu(gate) * up), tag_act));
+      }
+      // one pair at a time: keeps the unpacked codes of later pairs from
+      // being hoisted (and spilled) while this one is reduced
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- the next layer's routing-independent loads overlap this layer's
+    // hand-over and down projection.
+    if (!last) {
+      const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
+      const int n_rows_n = E + ((p.has_shared && Ln.sgate_w) ? 1 : 0);
+      issue_prologue<BITS, CPL, NP, RC>(Ln, row, n_rows_n, E, p.has_shared, K, gwave, n_waves,
+                                        n_pairs, h, lane, rw, pr, dr_next, dpw1_next);
+    }
+
+    // ---- down scales / biases of every unit, ready before act arrives.
+    const int gd = lane >> 3;
+    float dsc[NU], dbi[NU];
+#pragma unroll
+    for (int uu = 0; uu < NU; ++uu) {
+      dsc[uu] = uu == NU - 1 ? param_of(dpw1, 0, gd) : param_of(dpw0, uu * 8, gd);
+      dbi[uu] = uu == NU - 1 ? param_of(dpw1, 4, gd) : param_of(dpw0, uu * 8 + 4, gd);
+    }
+
+    // ---- poll every act word (9 per thread) into LDS.
+    {
+      uint32_t v[kStageAct];
+      for (int spin = 0;; ++spin) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < kStageAct; ++j) {
+          const int i = threadIdx.x + j * kThreads;
+          v[j] = i < n_pairs ? load_coherent_u32(sc->act + i) : 0u;
+          ok &= i >= n_pairs || tag_ok(v[j], tag_act);
+        }
+        if (ok) break;
+        if (spin >= kSpinLimit) { timed_out = true; break; }
+        __builtin_amdgcn_s_sleep(1);
+      }
+#pragma unroll
+      for (int j = 0; j < kStageAct; ++j)
+        s_act[threadIdx.x + j * kThreads] = __uint_as_float(v[j] & 0xFFFF0000u);
+    }
+    __syncthreads();
+    // sum of act over each lane's 8 values of each unit, shared by all waves
+    for (int i = threadIdx.x; i < U * 64; i += kThreads) {
+      const float4 a0 = *reinterpret_cast<const float4*>(s_act + i * 8);
+      const float4 a1 = *reinterpret_cast<const float4*>(s_act + i * 8 + 4);
+      s_asum[i] = ((((((a0.x + a0.y) + a0.z) + a0.w) + a1.x) + a1.y) + a1.z) + a1.w;
+    }
+    __syncthreads();
+
+    // ---- D: down row h of every unit from registers.
+    if (h < H) {
+      float ys[NU];
+#pragma unroll
+      for (int uu = 0; uu < NU; ++uu) {
+        // register slot NU-1 holds the shared unit (unit index K)
+        const int u = uu == NU - 1 ? K : uu;
+        const bool on = uu == NU - 1 ? (p.has_shared != 0) : (uu < K);
+        ys[uu] = 0.0f;
+        if (!on) continue;
+        const float4 a0 = *reinterpret_cast<const float4*>(s_act + u * I + lane * 8);
+        const float4 a1 = *reinterpret_cast<const float4*>(s_act + u * I + lane * 8 + 4);
+        const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float asum = s_asum[u * 64 + lane];
+        float qa = 0.0f;
+        if constexpr (BITS == 8) {
+          qa = qdot_word8(dr[uu].w[0], a[0], a[1], a[2], a[3], qa);
+          qa = qdot_word8(dr[uu].w[1], a[4], a[5], a[6], a[7], qa);
+        } else {
+          const uint32_t wd = dr[uu].w[0];
+          const uint32_t lo = wd & 0x0F0F0F0Fu;
+          const uint32_t hi = (wd >> 4) & 0x0F0F0F0Fu;
+          qa = fmaf((float)(lo & 0xFFu), a[0], qa);
+          qa = fmaf((float)(hi & 0xFFu), a[1], qa);
+          qa = fmaf((float)((lo >> 8) & 0xFFu), a[2], qa);
+          qa = fmaf((float)((hi >> 8) & 0xFFu), a[3], qa);
+          qa = fmaf((float)((lo >> 16) & 0xFFu), a[4], qa);
+          qa = fmaf((float)((hi >> 16) & 0xFFu), a[5], qa);
+          qa = fmaf((float)(lo >> 24), a[6], qa);
+          qa = fmaf((float)(hi >> 24), a[7], qa);
+        }
+        ys[uu] = dsc[uu] * qa + dbi[uu] * asum;
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int uu = 0; uu < NU; ++uu) {
+        const int u = uu == NU - 1 ? K : uu;
+        const bool on = uu == NU - 1 ? (p.has_shared != 0) : (uu < K);
+        if (on) acc += s_coef[u] * round_bf16(wave_sum(ys[uu]));
+      }
+      if (lane == 0) {
+        float o = round_bf16(acc);
+        if (p.residual_mode == 1)
+          o = round_bf16(s_x[h] + o);
+        else if (p.residual_mode == 2)
+          o = round_bf16(bf16_to_f32(p.residual[h]) + o);
+        const uint32_t ob = f32_to_bf16(o);
+        if (last)
+          p.out[h] = (uint16_t)ob;
+        else
+          store_coherent_u32(sc->xs[layer & 1] + h, tagged(ob, tag_x));
+      }
+    }
+    dr[NU - 1] = dr_next;
+    dpw1 = dpw1_next;
+    // s_x / s_act / s_idx are rewritten by the next layer
+    __syncthreads();
+  }
+  if (timed_out) store_coherent_u32(&sc->err, 1u);
+  // Workgroup 0 has consumed an act word from every workgroup, each written
+  // after that workgroup read the epoch: advancing it now is safe.
+  if (wg == 0 && threadIdx.x == 0) store_coherent_u32(&sc->epoch, base + phase);
+}
+
+hipError_t fused_grid(int bits, int* grid) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  // Occupancy does not change for a device: cache it (grid + 1, 0 = unknown).
+  static int cache[64][2];
+  const int slot = bits == 8 ? 0 : 1;
+  if (dev >= 0 && dev < 64) {
+    const int c = __atomic_load_n(&cache[dev][slot], __ATOMIC_RELAXED);
+    if (c > 0) {
+      *grid = c - 1;
+      return hipSuccess;
+    }
+  }
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  int per_cu = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &per_cu,
+      bits == 8 ? (const void*)fused_decode_kernel<8> : (const void*)fused_decode_kernel<4>,
+      kThreads, 0);
+  if (e != hipSuccess) return e;
+  *grid = per_cu >= 1 ? (cus < kFusedMaxGrid ? cus : kFusedMaxGrid) : 0;
+  if (dev >= 0 && dev < 64) __atomic_store_n(&cache[dev][slot], *grid + 1, __ATOMIC_RELAXED);
+  return hipSuccess;
+}
+
+hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s) {
+  FusedArgs args = a;
+  void* kargs[] = {&args};
+  const void* fn = bits == 8 ? (const void*)fused_decode_kernel<8>
+                             : (const void*)fused_decode_kernel<4>;
+  // A cooperative launch guarantees every workgroup is resident.  Under
+  // stream capture a plain launch of the same one-workgroup-per-CU grid is
+  // recorded instead (every workgroup fits at once on an otherwise idle
+  // device; the bounded waits turn anything else into a status error).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+    hipLaunchKernelGGL((bits == 8 ? fused_decode_kernel<8> : fused_decode_kernel<4>),
+                       dim3(grid), dim3(kThreads), 0, s, args);
+    return hipGetLastError();
+  }
+  return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kThreads), kargs, 0, s);
+}
+
+}  // namespace rmoe

@@ -12,6 +12,8 @@ constexpr int kMaxExperts = 1024;  // router ranks at most this many experts
 constexpr int kMaxTopK = 64;       // one slot per lane in the ranking wave
 constexpr int kUnitBatch = 9;      // down kernel: loads in flight per lane
 constexpr int kMaxTokens = 65535;  // grid.y of the router; counters reserved
+constexpr int kRouterBatch = 4;    // router: 16-byte loads in flight per lane
+constexpr int kStageBatch = 8;     // down: float4 act loads in flight per lane
 
 struct QW {
   const uint32_t* w;
@@ -49,6 +51,50 @@ struct QmvArgs {
   uint16_t* y_bf16;
   float* y_f32;
 };
+
+// ---- single-launch decode (fused.hip): one token, one or more layers.
+constexpr int kFusedThreads = 512;          // 8 waves, one workgroup per CU
+constexpr int kFusedMaxGrid = 1024;
+constexpr int kMaxFusedUnits = 9;           // top-k <= 8 plus the shared expert
+constexpr int kMaxFusedPairsPerWave = 3;
+constexpr int kMaxFusedRowsPerWave = 1;
+constexpr int kFusedMaxExperts = 256;
+constexpr int kFusedH = 2048;
+constexpr int kFusedI = 512;
+
+struct FusedLayer {
+  const uint16_t* router_w;
+  const uint16_t* sgate_w;
+  QW gu, dn, sgu, sdn;
+};
+
+// Device scratch of the fused kernel: lives at a fixed workspace offset so
+// the epoch persists across calls of any shape.  Values handed between
+// workgroups are tagged words: (bf16 value << 16) | (phase & 0xFFFF).
+struct FusedScratch {
+  uint32_t epoch;
+  uint32_t err;
+  uint32_t pad[62];
+  uint32_t logits[kFusedMaxExperts + 64];
+  uint32_t act[kMaxFusedUnits * kFusedI];
+  uint32_t xs[2][kFusedH];
+};
+
+struct FusedArgs {
+  int n_layers, E, K, norm, has_shared;
+  int residual_mode;          // 0 none, 1 the layer input, 2 `residual`
+  FusedLayer layer0;          // used when table == nullptr
+  const FusedLayer* table;    // device array of n_layers descriptors
+  const uint16_t* x;
+  uint16_t* out;
+  const uint16_t* residual;
+  FusedScratch* scratch;
+  int32_t* idx_out;
+  float* scores_out;
+};
+
+hipError_t fused_grid(int bits, int* grid);
+hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s);
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s);
 hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s);

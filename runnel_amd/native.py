@@ -211,6 +211,50 @@ def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None
     return out
 
 
+class Chain:
+    """A stack of layers for the single-launch chained decode
+    (rmoe_moe_chain): x_{l+1} = bf16(x_l + block_l(x_l))."""
+
+    def __init__(self, layers: list[LayerHandle], device="cuda"):
+        lib = _lib.load()
+        n = len(layers)
+        if n < 1:
+            raise ValueError("a chain needs at least one layer")
+        arr = (_lib.Layer * n)(*[h.struct for h in layers])
+        nbytes = lib.rmoe_chain_table_bytes(n)
+        host = (ctypes.c_uint8 * nbytes)()
+        _lib.check(lib.rmoe_chain_table_pack(arr, n, ctypes.addressof(host)))
+        self.table = torch.frombuffer(bytearray(host), dtype=torch.uint8).to(device)
+        self.layers = layers
+        self.n = n
+
+    def workspace_bytes(self) -> int:
+        return self.layers[0].workspace_bytes(1)
+
+
+def moe_chain(chain: Chain, x: torch.Tensor, out: torch.Tensor | None = None,
+              workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """One token x bf16 [1, H] (or [H]) through every layer of the chain."""
+    lib = _lib.load()
+    _require_cuda(x)
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    ws = workspace if workspace is not None else WORKSPACE.get(
+        x.device, chain.workspace_bytes(), "block")
+    _lib.check(lib.rmoe_moe_chain(ctypes.byref(chain.layers[0].struct), chain.table.data_ptr(),
+                                  chain.n, x.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                  ws.numel(), _lib.stream_handle(x.device)))
+    return out
+
+
+def workspace_status(ws: torch.Tensor) -> int:
+    """The status word of a workspace (nonzero: a single-launch decode timed
+    out waiting for another workgroup)."""
+    off = _lib.load().rmoe_workspace_status_offset()
+    return int(ws[off:off + 4].view(torch.int32).item())
+
+
 def router(router_w: torch.Tensor, x: torch.Tensor, top_k: int,
            norm_topk_prob: bool = True):
     """Router of the block: x bf16 [T, H], router_w bf16 [E, H] ->
