@@ -1,0 +1,246 @@
+"""The drop-in boundary without a GPU: the C ABI loads and exports what
+include/rmoe.h declares, rejects bad arguments on the host before anything
+is launched, and the torch-side modules keep the surface, validation and
+error messages of src/runnel/mlx.py.  No test here launches a kernel."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from runnel_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+FAKE = 0x100000  # an aligned, never-dereferenced address
+
+
+def declared_functions():
+    text = (ROOT / "include" / "rmoe.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(rmoe_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.EXPORTED)
+    assert lib.rmoe_abi_version() == _lib.ABI_VERSION
+
+
+def _qw(bits=8, experts=4, rows=128, cols=256, ptr=FAKE):
+    return _lib.QWeight(ptr, ptr, ptr, experts, rows, cols, bits, 64)
+
+
+def _layer(bits=8, E=4, H=256, I=64, K=2, shared=True):
+    return _lib.Layer(H, I, I if shared else 0, E, K, 1, FAKE, FAKE if shared else None,
+                      _qw(bits, E, 2 * I, H), _qw(bits, E, H, I),
+                      _qw(bits, 1, 2 * I, H) if shared else _lib.QWeight(),
+                      _qw(bits, 1, H, I) if shared else _lib.QWeight())
+
+
+def test_validate_layer_accepts_and_rejects():
+    lib = _lib.load()
+    assert lib.rmoe_validate_layer(ctypes.byref(_layer())) == _lib.RMOE_OK
+    assert lib.rmoe_validate_layer(None) == _lib.RMOE_ENULL
+    bad = _layer(bits=3)
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EBITS
+    bad = _layer()
+    bad.gate_up.group_size = 32
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EBITS
+    bad = _layer()
+    bad.gate_up.rows = 100
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EINVAL
+    assert b"2*inter" in lib.rmoe_last_error()
+    bad = _layer()
+    bad.router_w = FAKE + 2
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EALIGN
+    bad = _layer()
+    bad.top_k = 5
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EINVAL
+    bad = _layer(shared=False)
+    bad.shared_gate_w = FAKE
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EINVAL
+    bad = _layer()
+    bad.down.bits = 4
+    bad.down.cols = 64
+    assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EBITS
+
+
+def test_block_rejects_before_launch():
+    lib = _lib.load()
+    L = _layer()
+    need = lib.rmoe_workspace_bytes(ctypes.byref(L), 1)
+    assert need > 0
+    P = ctypes.c_void_p
+    # workspace too small / missing
+    rc = lib.rmoe_moe_block(ctypes.byref(L), FAKE, 1, None, FAKE + 4096, None, None,
+                            FAKE, need - 1, None)
+    assert rc == _lib.RMOE_EWS
+    rc = lib.rmoe_moe_block(ctypes.byref(L), FAKE, 1, None, FAKE + 4096, None, None,
+                            None, 0, None)
+    assert rc == _lib.RMOE_EWS
+    # misaligned x, aliasing out, token count
+    rc = lib.rmoe_moe_block(ctypes.byref(L), FAKE + 2, 1, None, FAKE, None, None, FAKE, need, None)
+    assert rc == _lib.RMOE_EALIGN
+    rc = lib.rmoe_moe_block(ctypes.byref(L), FAKE, 1, None, FAKE, None, None, FAKE, need, None)
+    assert rc == _lib.RMOE_EINVAL
+    rc = lib.rmoe_moe_block(ctypes.byref(L), FAKE, -1, None, FAKE + 64, None, None, FAKE, need, None)
+    assert rc == _lib.RMOE_EINVAL
+    # zero tokens is a no-op
+    assert lib.rmoe_moe_block(ctypes.byref(L), FAKE, 0, None, FAKE + 64, None, None,
+                              None, 0, None) == _lib.RMOE_OK
+    del P
+
+
+def test_switch_and_qmm_reject_before_launch():
+    lib = _lib.load()
+    gu, dn = _qw(8, 4, 128, 256), _qw(8, 4, 256, 64)
+    need = lib.rmoe_switch_workspace_bytes(ctypes.byref(gu), ctypes.byref(dn), 2, 2)
+    assert lib.rmoe_switch_glu(ctypes.byref(gu), ctypes.byref(dn), FAKE, 2, FAKE, 0, FAKE,
+                               FAKE, need, None) == _lib.RMOE_EINVAL
+    bad_dn = _qw(8, 4, 255, 64)
+    assert lib.rmoe_switch_glu(ctypes.byref(gu), ctypes.byref(bad_dn), FAKE, 2, FAKE, 2, FAKE,
+                               FAKE, need, None) == _lib.RMOE_EINVAL
+    assert lib.rmoe_switch_glu(ctypes.byref(gu), ctypes.byref(dn), FAKE, 2, FAKE, 2, FAKE,
+                               FAKE, need - 256, None) == _lib.RMOE_EWS
+    w = _qw(8, 1, 32, 256)
+    assert lib.rmoe_gather_qmm(FAKE, 1, None, None, 1, ctypes.byref(w), FAKE, FAKE,
+                               None) == _lib.RMOE_EINVAL  # both outputs given
+    assert lib.rmoe_gather_qmm(FAKE, 1, None, None, 1, ctypes.byref(w), None, None,
+                               None) == _lib.RMOE_EINVAL
+    w_odd = _qw(8, 1, 32, 192)  # 12 chunks per row: not a power of two
+    assert lib.rmoe_gather_qmm(FAKE, 1, None, None, 1, ctypes.byref(w_odd), FAKE, None,
+                               None) == _lib.RMOE_EINVAL
+
+
+def test_router_quantize_stream_reject_before_launch():
+    lib = _lib.load()
+    assert lib.rmoe_router(FAKE, 16, 100, 2, 1, FAKE, 1, FAKE, FAKE, FAKE, 1 << 20,
+                           None) == _lib.RMOE_EINVAL  # hidden not a multiple of 64
+    assert lib.rmoe_router(FAKE, 16, 128, 17, 1, FAKE, 1, FAKE, FAKE, FAKE, 1 << 20,
+                           None) == _lib.RMOE_EINVAL  # top_k > experts
+    assert lib.rmoe_quantize(FAKE, 4, 64, 5, 64, FAKE, FAKE, FAKE, None) == _lib.RMOE_EBITS
+    assert lib.rmoe_quantize(FAKE, 4, 100, 8, 64, FAKE, FAKE, FAKE, None) == _lib.RMOE_EINVAL
+    w = _qw(8, 2, 16, 128)
+    assert lib.rmoe_dequantize(ctypes.byref(w), 30, 4, FAKE, None, None) == _lib.RMOE_EINVAL
+    assert lib.rmoe_stream_read(FAKE, 100, FAKE, 4, None) == _lib.RMOE_EALIGN
+    assert lib.rmoe_stream_read(FAKE, 4096, FAKE, 0, None) == _lib.RMOE_EINVAL
+
+
+def test_chain_table_pack_rejects_mixed_layers():
+    lib = _lib.load()
+    layers = (_lib.Layer * 2)(_layer(), _layer(E=8))
+    n = lib.rmoe_chain_table_bytes(2)
+    buf = (ctypes.c_uint8 * n)()
+    assert lib.rmoe_chain_table_pack(layers, 2, ctypes.addressof(buf)) == _lib.RMOE_EINVAL
+    assert lib.rmoe_chain_table_bytes(0) == 0
+
+
+def test_status_strings():
+    lib = _lib.load()
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.rmoe_status_string(code)
+    assert lib.rmoe_workspace_status_offset() > 0
+
+
+def test_python_raises_value_error_with_the_message():
+    lib = _lib.load()
+    bad = _layer(bits=3)
+    with pytest.raises(ValueError, match="bits must be 4 or 8"):
+        _lib.check(lib.rmoe_validate_layer(ctypes.byref(bad)))
+
+
+# ---------------------------------------------------------------- modules
+
+def _switch(bits=8, E=4, H=128, I=64, device="cpu"):
+    from runnel_amd import SwitchGLU
+    m = SwitchGLU(H, I, E, bits=bits, device=device)
+    g = torch.Generator().manual_seed(0)
+    for proj in (m.gate_proj, m.up_proj, m.down_proj):
+        proj.weight.copy_(torch.randint(-2**31, 2**31 - 1, proj.weight.shape, generator=g,
+                                        dtype=torch.int64).to(torch.int32))
+        proj.scales.copy_(torch.randn(proj.scales.shape, generator=g).to(torch.bfloat16))
+        proj.biases.copy_(torch.randn(proj.biases.shape, generator=g).to(torch.bfloat16))
+    return m
+
+
+def test_fused_module_packs_up_then_gate():
+    from runnel_amd import FusedQuantizedSwitchGLU
+    old = _switch()
+    fused = FusedQuantizedSwitchGLU(old)
+    assert torch.equal(fused.weight, torch.cat([old.up_proj.weight, old.gate_proj.weight], 1))
+    assert torch.equal(fused.scales, torch.cat([old.up_proj.scales, old.gate_proj.scales], 1))
+    assert torch.equal(fused.biases, torch.cat([old.up_proj.biases, old.gate_proj.biases], 1))
+    assert fused.bits == 8 and fused.group_size == 64 and fused.mode == "affine"
+    assert fused.down_proj is old.down_proj and fused.activation is old.activation
+    assert "weight" in fused and fused.get("bias") is None
+
+
+def test_fused_module_error_messages():
+    from runnel_amd import FusedQuantizedSwitchGLU
+    old = _switch()
+    old.gate_proj.bits = 4
+    with pytest.raises(ValueError, match="^routed gate/up quantization formats differ$"):
+        FusedQuantizedSwitchGLU(old)
+    old = _switch()
+    old.up_proj.register_buffer("bias", torch.zeros(4, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="^module biases are not expected for this checkpoint$"):
+        FusedQuantizedSwitchGLU(old)
+    old = _switch()
+    old.gate_proj.register_buffer("biases", None)
+    with pytest.raises(ValueError, match="^routed gate/up affine-bias formats differ$"):
+        FusedQuantizedSwitchGLU(old)
+
+
+class _Obj:
+    pass
+
+
+def _fake_model(n_layers, quantized=True):
+    model = _Obj()
+    model.language_model = _Obj()
+    model.language_model.layers = []
+    for _ in range(n_layers):
+        layer = _Obj()
+        layer.mlp = _Obj()
+        layer.mlp.switch_mlp = _switch()
+        if not quantized:
+            del layer.mlp.switch_mlp.gate_proj.bits
+        model.language_model.layers.append(layer)
+    return model
+
+
+def test_fuse_routed_gate_up_counts_and_replaces():
+    from runnel_amd import FusedQuantizedSwitchGLU, fuse_routed_gate_up
+    model = _fake_model(3)
+    assert fuse_routed_gate_up(model) == 3
+    for layer in model.language_model.layers:
+        assert isinstance(layer.mlp.switch_mlp, FusedQuantizedSwitchGLU)
+
+
+def test_fuse_routed_gate_up_requires_quantized_projections():
+    from runnel_amd import fuse_routed_gate_up
+    model = _fake_model(1, quantized=False)
+    with pytest.raises(ValueError, match="^routed gate/up are not quantized as expected$"):
+        fuse_routed_gate_up(model)
+
+
+def test_kernels_refuse_host_tensors():
+    from runnel_amd import native
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    w = torch.zeros(1, 32, 32, dtype=torch.int32)
+    s = torch.zeros(1, 32, 2, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.gather_qmm(x, w, s, s, 8)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.quantize(torch.zeros(4, 64), 8)
+
+
+def test_bench_byte_model_matches_the_survey_figures():
+    import bench
+    assert bench.layer_bytes(2048, 512, 256, 8, 8) == 31_141_888
+    assert bench.layer_bytes(2048, 512, 256, 8, 4) == 16_986_112
