@@ -5,17 +5,22 @@ Default workload: a stack of 40 independent 8-bit MoE layers (hidden 2048,
 256 experts, top-8 + 1 shared expert, intermediate 512, group 64, random
 weights seeded per layer, 34.4 GB resident in HBM), one batch-1 decode token
 chained through all 40 layers with a residual add between them.  A step is
-one token through the 40 layers in a single cooperative launch
-(rmoe_moe_chain).  Each step's input is the previous step's output, so the
-routing changes from token to token.
+one token through the 40 layers in a single launch of the chained kernel
+(rmoe_moe_chain), replayed from a captured HIP graph as a serving loop would
+(--launch eager calls the library every step instead).  Each step's input is
+the previous step's output, so the routing changes from token to token.
 
 Prints one JSON line.  `value` is microseconds per MoE layer per token
 (lower is better); `hbm_gbps` is the algorithmic bytes of a layer divided
 by that time; `roofline` relates the same quantity to MI355X's 8 TB/s.
 
-Other workloads (--workload): c1 (one 8-bit layer), c2 (one 4-bit layer),
-prefill512 (8-bit, 512 tokens), prefill8192 (4-bit, 8192 tokens, Zipf-skewed
-routing) - for exploration; the default is the bench line.
+`roofline` is priced per launch of the dominant kernel (fused_decode_kernel,
+one launch per token carrying all 40 layers): algorithmic bytes of 40 layers
+divided by the launch's average duration, timed with HIP events on the
+stream the kernel runs on.  `traffic` is the HBM bytes one launch actually
+moves, read from profiles/fused_decode_chain40_q8_traffic.txt (two rocprofv3
+--pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by a plain copy kernel's
+reading; `--calibrate-copy` runs that copy kernel).
 """
 
 from __future__ import annotations
@@ -48,6 +53,35 @@ def layer_bytes(hidden, inter, experts, top_k, bits, shared=True, tokens=1, resi
         b += per_expert + hidden * 2
     b += tokens * hidden * 2 * (3 if residual else 2)
     return b
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "fused_decode_chain40_q8_traffic.txt"
+
+
+def recorded_traffic(layers: int, bits: int):
+    """HBM bytes per launch of the chained decode kernel as measured by the
+    rocprofv3 counter passes recorded under profiles/, or None when no
+    measurement of this exact workload is recorded."""
+    if not TRAFFIC_FILE.exists() or (layers, bits) != (40, 8):
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch"):
+            return int(line.split("=")[1].strip())
+    return None
+
+
+def calibrate_copy(torch, gib: int = 1, reps: int = 5):
+    """A plain copy kernel of known size for scaling the counters: each
+    launch reads `gib` GiB and writes `gib` GiB (bitwise NOT of int32)."""
+    n = gib * (1 << 30) // 4
+    a = torch.ones(n, dtype=torch.int32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        torch.bitwise_not(a, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "bitwise_not int32", "bytes_read": n * 4,
+                      "bytes_written": n * 4, "launches": reps}), flush=True)
+    return 0
 
 
 def median(v):
@@ -103,8 +137,26 @@ def run_decode_chain(args, torch):
     bufs = [synthetic.make_x(12345, 1, H), torch.empty((1, H), dtype=torch.bfloat16, device="cuda")]
     ws = torch.zeros(chain.workspace_bytes(), dtype=torch.uint8, device="cuda")
 
-    def step(i):
+    def launch(i):
         native.moe_chain(chain, bufs[i & 1], out=bufs[(i + 1) & 1], workspace=ws)
+
+    step = launch
+    if args.launch == "graph":
+        # the decode loop as a serving loop runs it: one captured HIP graph
+        # per direction of the ping-pong buffers, each holding the one
+        # launch of the chained kernel; a step replays one of them.  Nothing
+        # is launched before the capture (the library allocates nothing per
+        # call), so in this mode the kernel only ever runs from the graphs.
+        graphs = []
+        for d in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                launch(d)
+            graphs.append(g)
+        torch.cuda.synchronize()
+
+        def step(i):
+            graphs[i & 1].replay()
 
     for i in range(args.warmup):
         step(i)
@@ -143,6 +195,11 @@ def main():
     ap.add_argument("--bits", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
+                    help="replay captured HIP graphs (default) or launch eagerly "
+                         "(cooperative launch) every step")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only the plain copy kernel used to scale HBM counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path "
@@ -154,9 +211,12 @@ def main():
     from runnel_amd import _lib
     _lib.load()
     torch.cuda.synchronize()
+    if args.calibrate_copy:
+        return calibrate_copy(torch)
     res = run_decode_chain(args, torch)
-    per_launch = res["us_layer"]
-    achieved = res["gbps"]
+    launch_bytes = res["layer_bytes"] * args.layers
+    achieved = launch_bytes / (res["us_token"] * 1e-6) / 1e9
+    traffic = recorded_traffic(args.layers, args.bits)
     out = {
         "metric": METRIC,
         "value": round(res["us_layer"], 3),
@@ -174,6 +234,7 @@ def main():
             "workload": f"{args.layers}-layer {args.bits}-bit MoE chain, batch-1 decode with "
                         "residual (hidden 2048, 256 experts, top-8 + shared, inter 512, group 64)",
             "layers": args.layers, "bits": args.bits, "tokens_per_step": 1,
+            "launch": args.launch,
             "resident_weight_gb": round(res["resident_gb"], 2),
         },
         "tokens_per_s": round(1e6 / res["us_token"], 2),
@@ -187,9 +248,9 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
-            "bytes_per_launch": res["layer_bytes"],
-            "us_per_launch": round(per_launch, 3),
+            "traffic": traffic,
+            "bytes_per_launch": launch_bytes,
+            "us_per_launch": round(res["us_token"], 3),
         },
     }
     if not args.no_cpu_baseline:

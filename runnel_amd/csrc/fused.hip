@@ -1,7 +1,8 @@
 // Single-launch batch-1 decode of one or more MoE layers (gfx950).
 //
 // One workgroup of 8 waves per CU, launched cooperatively so every
-// workgroup is resident.  Per layer:
+// workgroup is resident (inside a captured graph: a plain launch of the same
+// grid, see launch_fused_decode).  Per layer:
 //
 //   R  router rows, one per workgroup (the fixed-order dot of the router
 //      contract); the row weights are loaded before x is even staged

@@ -151,3 +151,31 @@ def test_chain_equals_single_layer_calls(torch_cuda):
         y = native.moe_block(h, y, residual=y)
     torch.cuda.synchronize()
     assert torch.equal(y_chain, y)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_graph_replays_equal_eager_calls(torch_cuda, bits):
+    """The chained kernel captured into a HIP graph (recorded as a plain
+    launch) and replayed with a new input each time, with eager launches on
+    the same workspace and host synchronisations between the replays: every
+    replay equals the eager cooperative launch exactly."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lws = [synthetic.make_layer(950 + bits + l, bits=bits) for l in range(2)]
+    chain = native.Chain([lw.handle() for lw in lws])
+    ws = torch.zeros(chain.workspace_bytes(), dtype=torch.uint8, device="cuda")
+    xin = synthetic.make_x(17, 1, 2048)
+    out = torch.empty_like(xin)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        native.moe_chain(chain, xin, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    for r in range(4):
+        xr = synthetic.make_x(100 + r, 1, 2048)
+        xin.copy_(xr)
+        g.replay()
+        torch.cuda.synchronize()
+        eager = native.moe_chain(chain, xr, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+    assert native.workspace_status(ws) == 0
