@@ -41,6 +41,11 @@ exact bf16 rounding points inside ``gather_qmm`` and the tie order of
   op-by-op mlx-lm evaluation performs (silu output, score products, the
   routed sum, the gated shared term)
   (max-abs <= 2e-2, cosine >= 0.9999) is checked against it.
+  ``mode="prefill"`` is the contract of the expert-sorted grouped GEMM used
+  when a call routes at least 64 (token, slot) rows (the reference's sort
+  threshold, src/runnel/mlx.py:59): the same rounding points, with each
+  dequantised weight rounded to bf16 before the product (the operand of a
+  bf16 matrix-core tile); this rounding point is the build's own choice.
 * ``quantize`` restates MLX's documented affine quantizer (edge value kept
   exact, scale sign chosen by the larger-magnitude edge).  It only produces
   test weights; parity of the block never depends on it.  Parity unpinned
@@ -300,12 +305,22 @@ class Layer:
         return 0 if self.shared_gate_up is None else self.shared_gate_up.rows // 2
 
 
+def _bf16_weights(w64: np.ndarray) -> np.ndarray:
+    """Prefill weight tile: fl32(q*s + b) rounded to bf16 (RNE), the operand
+    a bf16 matrix-core product consumes."""
+    return round_bf16(w64.astype(np.float32)).astype(np.float64)
+
+
 def expert_ffn(gate_up: QWeight, down: QWeight, e: int, xf: np.ndarray,
                mode: str = "contract") -> np.ndarray:
     """Rows of xf (float32 [n, H], bf16-valued) through expert e.
-    Returns y [n, H] float32 (bf16-valued)."""
+    Returns y [n, H] float32 (bf16-valued).  ``mode="prefill"`` is the
+    contract with every dequantised weight rounded to bf16 first (the
+    expert-sorted grouped GEMM's operand); the rest is the same."""
     I = gate_up.rows // 2
     wgu = gate_up.dequant(e)  # [2I, H] float64
+    if mode == "prefill":
+        wgu = _bf16_weights(wgu)
     gu = xf.astype(np.float64) @ wgu.T
     up = round_bf16(gu[:, :I].astype(np.float32))
     gate = round_bf16(gu[:, I:].astype(np.float32))
@@ -314,6 +329,8 @@ def expert_ffn(gate_up: QWeight, down: QWeight, e: int, xf: np.ndarray,
     else:
         act = round_bf16(_silu32(gate) * up)
     wdn = down.dequant(e)  # [H, I]
+    if mode == "prefill":
+        wdn = _bf16_weights(wdn)
     y = act.astype(np.float64) @ wdn.T
     return round_bf16(y.astype(np.float32))
 

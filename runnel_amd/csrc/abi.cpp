@@ -135,12 +135,24 @@ size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 // Workspace carve-up shared by the router, switch and block calls.
 struct Layout {
   size_t ctr, fused, logits, idx, scores, act, total;
+  // expert-sorted (prefill) path
+  size_t rows, offs, tile_offs, act16, y16;
 };
+
+// Calls that route at least kPrefillMinRows (token, slot) rows take the
+// expert-sorted grouped GEMM (the packed module sorts from 64 indices on,
+// src/runnel/mlx.py:59); its tiles need these shapes.
+bool prefill_path(int T, int K, int E, int H, int I) {
+  return (long)T * K >= rmoe::kPrefillMinRows && E <= rmoe::kPrefillMaxExperts &&
+         H % 256 == 0 && I % rmoe::kPrefillTileN == 0;
+}
 
 // The per-token counters sit at a fixed offset with room for the largest
 // token count, so a workspace reused by calls of different shapes always
 // finds them at zero (every kernel leaves them at zero when it finishes).
-Layout layout(int T, int E, int K, int I) {
+// The router's logits / indices / scores come next in both paths.
+Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
+              bool combine = false) {
   Layout l{};
   size_t off = 0;
   l.ctr = off;
@@ -153,10 +165,51 @@ Layout layout(int T, int E, int K, int I) {
   off = align_up(off + (size_t)T * K * sizeof(int32_t));
   l.scores = off;
   off = align_up(off + (size_t)T * (K + 1) * sizeof(float));
-  l.act = off;
-  off = align_up(off + (size_t)T * (K + 1) * I * sizeof(float));
+  if (!sorted) {
+    l.act = off;
+    off = align_up(off + (size_t)T * (K + 1) * I * sizeof(float));
+  } else {
+    const size_t R = (size_t)T * K + T;
+    l.rows = off;
+    off = align_up(off + R * sizeof(int32_t));
+    l.offs = off;
+    off = align_up(off + (size_t)(E + 3) * sizeof(int32_t));
+    l.tile_offs = off;
+    off = align_up(off + (size_t)(E + 3) * sizeof(int32_t));
+    l.act16 = off;
+    off = align_up(off + R * I * sizeof(uint16_t));
+    if (combine) {
+      l.y16 = off;
+      off = align_up(off + R * H * sizeof(uint16_t));
+    }
+  }
   l.total = off;
   return l;
+}
+
+Layout block_layout(const rmoe_layer* L, int T) {
+  const bool sorted = prefill_path(T, L->top_k, L->experts, L->hidden, L->inter);
+  return layout(T, L->experts, L->top_k, L->inter, L->hidden, sorted, true);
+}
+
+rmoe::PrefillArgs prefill_args(const Layout& l, void* ws, int T, int H, int I, int E, int K,
+                               const uint16_t* x, const int32_t* idx) {
+  char* base = static_cast<char*>(ws);
+  rmoe::PrefillArgs a{};
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.K = K;
+  a.x = x;
+  a.idx = idx;
+  a.rows = reinterpret_cast<int32_t*>(base + l.rows);
+  a.offs = reinterpret_cast<int32_t*>(base + l.offs);
+  a.tile_offs = reinterpret_cast<int32_t*>(base + l.tile_offs);
+  a.act = reinterpret_cast<uint16_t*>(base + l.act16);
+  a.y = l.y16 ? reinterpret_cast<uint16_t*>(base + l.y16) : nullptr;
+  a.scores = reinterpret_cast<const float*>(base + l.scores);
+  return a;
 }
 
 rmoe::QW qw(const rmoe_qweight& q) { return rmoe::QW{q.w, q.scales, q.biases}; }
@@ -279,14 +332,17 @@ int rmoe_validate_layer(const rmoe_layer* layer) {
 
 size_t rmoe_workspace_bytes(const rmoe_layer* L, int32_t tokens) {
   if (check_layer(L) || tokens < 0) return 0;
-  return layout(tokens, L->experts, L->top_k, L->inter).total;
+  return block_layout(L, tokens).total;
 }
 
 size_t rmoe_switch_workspace_bytes(const rmoe_qweight* gate_up,
                                    const rmoe_qweight* down, int32_t tokens,
                                    int32_t top_k) {
   if (!gate_up || !down || tokens < 0 || top_k < 1) return 0;
-  return layout(tokens, gate_up->experts, top_k, gate_up->rows / 2).total;
+  const int I = gate_up->rows / 2;
+  const int H = gate_up->cols;
+  const bool sorted = prefill_path(tokens, top_k, gate_up->experts, H, I);
+  return layout(tokens, gate_up->experts, top_k, I, H, sorted, false).total;
 }
 
 size_t rmoe_router_workspace_bytes(int32_t experts, int32_t top_k, int32_t tokens) {
@@ -343,8 +399,8 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
     return fail(RMOE_EALIGN, "out/residual must be 2-byte aligned");
   if (static_cast<const void*>(out) == static_cast<const void*>(x))
     return fail(RMOE_EINVAL, "out must not alias x");
-  const size_t need = layout(tokens, L->experts, L->top_k, L->inter).total;
-  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  const Layout lay = block_layout(L, tokens);
+  if ((rc = check_ws(ws, ws_bytes, lay.total))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int bits = L->gate_up.bits;
   int grid = 0;
@@ -366,6 +422,20 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   a.scores_out = scores_out;
   hipError_t e = rmoe::launch_router(a, s);
   if (e != hipSuccess) return hip_fail(e, "router launch");
+  if (lay.rows) {
+    rmoe::PrefillArgs pa = prefill_args(lay, ws, tokens, L->hidden, L->inter, L->experts,
+                                        L->top_k, x, a.idx);
+    pa.has_shared = a.has_shared;
+    pa.gu = a.gu;
+    pa.dn = a.dn;
+    pa.sgu = a.sgu;
+    pa.sdn = a.sdn;
+    pa.residual = residual;
+    pa.out = out;
+    e = rmoe::launch_prefill(pa, bits, true, s);
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return ok();
+  }
   e = rmoe::launch_gate_up(a, bits, s);
   if (e != hipSuccess) return hip_fail(e, "gate/up launch");
   e = rmoe::launch_down(a, bits, true, s);
@@ -396,8 +466,20 @@ int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
   if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
   if (!aligned(indices, 4) || !aligned(y, 2))
     return fail(RMOE_EALIGN, "indices/y misaligned");
-  const size_t need = layout(tokens, gate_up->experts, top_k, I).total;
-  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  const bool sorted = prefill_path(tokens, top_k, gate_up->experts, H, I);
+  const Layout lay = layout(tokens, gate_up->experts, top_k, I, H, sorted, false);
+  if ((rc = check_ws(ws, ws_bytes, lay.total))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (sorted) {
+    rmoe::PrefillArgs pa = prefill_args(lay, ws, tokens, H, I, gate_up->experts, top_k, x,
+                                        indices);
+    pa.gu = qw(*gate_up);
+    pa.dn = qw(*down);
+    pa.y = y;
+    const hipError_t e = rmoe::launch_prefill(pa, gate_up->bits, false, s);
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return ok();
+  }
   rmoe_layer L{};
   L.hidden = H;
   L.inter = I;
@@ -409,7 +491,6 @@ int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
   a.idx = const_cast<int32_t*>(indices);
   a.switch_mode = 1;
   a.out = y;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = rmoe::launch_gate_up(a, gate_up->bits, s);
   if (e != hipSuccess) return hip_fail(e, "gate/up launch");
   e = rmoe::launch_down(a, gate_up->bits, false, s);

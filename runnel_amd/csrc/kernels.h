@@ -109,4 +109,28 @@ hipError_t launch_dequantize(const QW& q, int cols, int bits, int64_t row_begin,
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* partials,
                               int blocks, hipStream_t st);
 
+// ---- prefill (prefill.hip): expert-sorted grouped dequant-GEMM on MFMA.
+constexpr int kPrefillMaxExperts = 512;  // buckets of the one-workgroup sort
+constexpr int kPrefillBM = 128;          // sorted rows per m-tile
+constexpr int kPrefillTileN = 128;       // [up; gate] pairs per gate/up tile
+constexpr int kPrefillMinRows = 64;      // (token, slot) rows that select it
+
+struct PrefillArgs {
+  int T, H, I, E, K, has_shared;
+  const uint16_t* x;       // [T, H]
+  const int32_t* idx;      // [T, K] expert ids (out of range -> zero rows)
+  QW gu, dn, sgu, sdn;
+  int32_t* rows;           // [T K + T] source row of each sorted row
+  int32_t* offs;           // [E + 3] rows per bucket (E: shared, E + 1: bad ids)
+  int32_t* tile_offs;      // [E + 3] m-tiles per bucket; [E + 2] = total
+  uint16_t* act;           // [T K + T, I] bf16, sorted order
+  uint16_t* y;             // [T K (+ T), H] bf16 at row t K + j (shared: T K + t)
+  const float* scores;     // [T, K + 1] router scores, slot K = shared gate
+  const uint16_t* residual;
+  uint16_t* out;           // [T, H]
+};
+
+int prefill_max_mtiles(int T, int K, int E);
+hipError_t launch_prefill(const PrefillArgs& a, int bits, bool combine, hipStream_t s);
+
 }  // namespace rmoe
