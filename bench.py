@@ -186,6 +186,59 @@ def run_decode_chain(args, torch):
     }
 
 
+def prefill_flops(T, H, I, E, K, shared=True):
+    rows = T * K + (T if shared else 0)
+    return 2 * T * E * H + 2 * rows * (2 * I * H + H * I)
+
+
+def run_prefill(torch, tokens, bits, skewed, steps, warmup, seed=7):
+    """One prefill chunk of `tokens` tokens through one full-size layer
+    (rmoe_moe_block: router, expert sort, gate/up + SwiGLU and down grouped
+    GEMMs on MFMA, combine), timed with HIP events over `steps` calls."""
+    from runnel_amd import native, synthetic
+    import numpy as np
+    H, I, E, K = 2048, 512, 256, 8
+    lw = synthetic.make_layer(seed, bits=bits)
+    if skewed:
+        synthetic.apply_router_bias(lw, synthetic.zipf_bias(seed, E))
+        x = synthetic.make_skewed_x(seed + 1, tokens, H)
+    else:
+        x = synthetic.make_x(seed + 1, tokens, H)
+    h = lw.handle()
+    out = torch.empty_like(x)
+    _, idx, _ = native.moe_block(h, x, out=out, return_routing=True)
+    torch.cuda.synchronize()
+    counts = np.bincount(idx.cpu().numpy().reshape(-1), minlength=E)
+    for _ in range(warmup):
+        native.moe_block(h, x, out=out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        native.moe_block(h, x, out=out)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    times = [ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(steps)]
+    us = median(times)
+    per_expert = layer_bytes(H, I, E, 1, bits, shared=False) - E * H * 2 - 2 * H * 2
+    touched = int((counts > 0).sum())
+    nbytes = (touched + 1) * per_expert + E * H * 2 + H * 2 + 2 * tokens * H * 2
+    flops = prefill_flops(tokens, H, I, E, K)
+    return {
+        "tokens": tokens, "bits": bits, "skewed": skewed, "us": round(us, 1),
+        "tokens_per_s": round(tokens / (us * 1e-6), 1),
+        "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+        "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "hbm_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes": nbytes, "flops": flops,
+        "experts_touched": touched, "max_rows_per_expert": int(counts.max()),
+        "experts_over_1000": int((counts > 1000).sum()),
+        "experts_under_8": int((counts < 8).sum()),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,6 +251,12 @@ def main():
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
                     help="replay captured HIP graphs (default) or launch eagerly "
                          "(cooperative launch) every step")
+    ap.add_argument("--workload", choices=["decode40", "prefill512", "prefill8192"],
+                    default="decode40",
+                    help="decode40: the bench line; the prefill workloads print "
+                         "their own line (exploration and profiling)")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the prefill figures appended to the decode line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the plain copy kernel used to scale HBM counters")
     args = ap.parse_args()
@@ -213,6 +272,11 @@ def main():
     torch.cuda.synchronize()
     if args.calibrate_copy:
         return calibrate_copy(torch)
+    if args.workload != "decode40":
+        tokens, bits, skewed = (512, 8, False) if args.workload == "prefill512" else (8192, 4, True)
+        r = run_prefill(torch, tokens, bits, skewed, args.steps, args.warmup)
+        print(json.dumps({"workload": args.workload, **r}), flush=True)
+        return 0
     res = run_decode_chain(args, torch)
     launch_bytes = res["layer_bytes"] * args.layers
     achieved = launch_bytes / (res["us_token"] * 1e-6) / 1e9
@@ -253,6 +317,12 @@ def main():
             "us_per_launch": round(res["us_token"], 3),
         },
     }
+    if not args.no_prefill:
+        # prefill figures of the same build (one layer per call, HIP events)
+        out["prefill"] = {
+            "512 tokens 8-bit": run_prefill(torch, 512, 8, False, 20, 3),
+            "8192 tokens 4-bit zipf": run_prefill(torch, 8192, 4, True, 10, 2),
+        }
     if not args.no_cpu_baseline:
         from oracle.moe_ref import f32_to_bf16
         lw0 = res["stack"][0]

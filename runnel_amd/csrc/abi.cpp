@@ -136,7 +136,7 @@ size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 struct Layout {
   size_t ctr, fused, logits, idx, scores, act, total;
   // expert-sorted (prefill) path
-  size_t rows, offs, tile_offs, act16, y16;
+  size_t rows, offs, tile_offs, act16, y16, wnorm;
 };
 
 // Calls that route at least kPrefillMinRows (token, slot) rows take the
@@ -176,6 +176,8 @@ Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
     off = align_up(off + (size_t)(E + 3) * sizeof(int32_t));
     l.tile_offs = off;
     off = align_up(off + (size_t)(E + 3) * sizeof(int32_t));
+    l.wnorm = off;
+    off = align_up(off + (size_t)E * sizeof(float));
     l.act16 = off;
     off = align_up(off + R * I * sizeof(uint16_t));
     if (combine) {
@@ -420,7 +422,12 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   a.residual = residual;
   a.idx_out = indices_out;
   a.scores_out = scores_out;
-  hipError_t e = rmoe::launch_router(a, s);
+  hipError_t e;
+  if (lay.rows && rmoe::router_mfma_eligible(L->experts, L->hidden))
+    e = rmoe::launch_router_mfma(
+        a, reinterpret_cast<float*>(static_cast<char*>(ws) + lay.wnorm), s);
+  else
+    e = rmoe::launch_router(a, s);
   if (e != hipSuccess) return hip_fail(e, "router launch");
   if (lay.rows) {
     rmoe::PrefillArgs pa = prefill_args(lay, ws, tokens, L->hidden, L->inter, L->experts,

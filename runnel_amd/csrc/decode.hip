@@ -18,6 +18,48 @@
 namespace rmoe {
 
 // ------------------------------------------------------------------ router
+// Ranking, softmax and scores of one token from its bf16-valued logits
+// (lane + 64 i holds expert lane + 64 i; experts >= E are ignored) and the
+// shared-expert gate's fp32 logit.  One wave.
+template <int P>
+__device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const float (&lv)[P],
+                                             float sg_logit, uint32_t* s_topk) {
+  const int lane = threadIdx.x & 63;
+  uint32_t keys[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int e = lane + 64 * i;
+    keys[i] = e < p.E ? (bf16_order_key(f32_to_bf16(lv[i])) << 16) | (0xFFFFu - (uint32_t)e)
+                      : 0u;
+  }
+  const uint32_t my_key = wave_topk<P>(keys, p.K, s_topk);
+  const uint32_t top_key = __builtin_amdgcn_readfirstlane(my_key);
+  const float m = bf16_to_f32(bf16_from_order_key(top_key >> 16));
+  float z = 0.0f;
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+    if (lane + 64 * i < p.E) z += __expf(lv[i] - m);
+  z = wave_sum(z);
+  const int my_sel = (int)(0xFFFFu - (my_key & 0xFFFFu));
+  const float my_logit = bf16_to_f32(bf16_from_order_key(my_key >> 16));
+  float pb = 0.0f;
+  if (lane < p.K) pb = round_bf16(__expf(my_logit - m) / z);
+  float total = 0.0f;
+  for (int j = 0; j < p.K; ++j) total += __shfl(pb, j, 64);
+  const float score = p.norm ? round_bf16(pb / total) : pb;
+  if (lane < p.K) {
+    p.idx[t * p.K + lane] = my_sel;
+    p.scores[t * (p.K + 1) + lane] = score;
+    if (p.idx_out) p.idx_out[t * p.K + lane] = my_sel;
+    if (p.scores_out) p.scores_out[t * p.K + lane] = score;
+  }
+  if (lane == 0) {
+    float sg = 1.0f;
+    if (p.sgate_w) sg = round_bf16(sigmoid(round_bf16(sg_logit)));
+    p.scores[t * (p.K + 1) + p.K] = sg;
+  }
+}
+
 template <int P>
 __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   const int t = blockIdx.y;
@@ -76,46 +118,220 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   __syncthreads();
   if (s_last == 0u || wave != 0) return;
 
-  uint32_t keys[P];
   float lv[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
     const int e = lane + 64 * i;
-    lv[i] = 0.0f;
-    keys[i] = 0;
-    if (e < p.E) {
-      const uint32_t b = f32_to_bf16(load_coherent(lg + e));
-      lv[i] = bf16_to_f32(b);
-      keys[i] = (bf16_order_key(b) << 16) | (0xFFFFu - (uint32_t)e);
+    lv[i] = e < p.E ? round_bf16(load_coherent(lg + e)) : 0.0f;
+  }
+  const float sg_logit = has_sg ? load_coherent(lg + p.E) : 0.0f;
+  finish_route<P>(p, t, lv, sg_logit, s_topk);
+  if (lane == 0)
+    __hip_atomic_store(&p.ctr[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------ prefill router (MFMA)
+// For many tokens the router is a [T, H] x [H, E] product.  The logits are
+// computed on the matrix cores in fp32 (order of the hardware's choosing),
+// then every token's selection is settled exactly:
+//
+//   |L - exact| <= (H - 1) 2^-23 S   any order of fp32 sums of the exact
+//                                    bf16 products (round to nearest or
+//                                    toward zero)
+//   |c - exact| <= (H/64 + 8) 2^-24 S  the router contract's order
+//   S = sum |x_k w_k| <= |x|_2 max_e |w_e|_2
+//
+// so with delta the sum of both bounds (plus a denormal allowance), an
+// expert whose L is more than margin = 2 delta + one bf16 ulp (at the
+// largest logit's magnitude, padded) below the k-th largest L rounds to a
+// bf16 logit strictly below those of k other experts and cannot be
+// selected.  Every expert within the margin is recomputed in the contract
+// order (the decode router's exact fp32 value); the ranking then runs on
+// exact bf16 logits for all candidates.  Experts outside the margin keep
+// bf16(L) (they only enter the softmax denominator).
+
+__global__ __launch_bounds__(256) void router_rownorm_kernel(const DecodeArgs p, float* wnorm) {
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (e >= p.E) return;
+  const uint16_t* w = p.router_w + (size_t)e * p.H;
+  float s = 0.0f;
+  for (int c = lane; c < p.H / 8; c += 64) {
+    const uint4 v = load16(w + c * 8);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), s);
+      s = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), s);
     }
   }
-  const uint32_t my_key = wave_topk<P>(keys, p.K, s_topk);
-  const uint32_t top_key = __builtin_amdgcn_readfirstlane(my_key);
-  const float m = bf16_to_f32(bf16_from_order_key(top_key >> 16));
-  float z = 0.0f;
+  s = wave_sum(s);
+  if (lane == 0) wnorm[e] = sqrtf(s) * (1.0f + 1.0f / 1024.0f);
+}
+
+typedef __bf16 bf16x8_r __attribute__((ext_vector_type(8)));
+typedef float f32x4_r __attribute__((ext_vector_type(4)));
+
+// One wave: 16 tokens x 64 experts, K in chunks of 64 (four chunks of
+// loads in flight per lane); lane (col, g) holds A row / B column `col` and
+// k = 16 g + [0, 16) of each chunk.
+__global__ __launch_bounds__(64) void router_logits_mfma_kernel(const DecodeArgs p) {
+  const int lane = threadIdx.x;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int t0 = blockIdx.x * 16;
+  const int e0 = blockIdx.y * 64;
+  const int tr = min(t0 + col, p.T - 1);
+  const uint16_t* xa = p.x + (size_t)tr * p.H + g * 16;
+  const uint16_t* wb[4];
 #pragma unroll
-  for (int i = 0; i < P; ++i)
-    if (lane + 64 * i < p.E) z += __expf(lv[i] - m);
-  z = wave_sum(z);
-  const int my_sel = (int)(0xFFFFu - (my_key & 0xFFFFu));
-  const float my_logit = bf16_to_f32(bf16_from_order_key(my_key >> 16));
-  float pb = 0.0f;
-  if (lane < p.K) pb = round_bf16(__expf(my_logit - m) / z);
-  float total = 0.0f;
-  for (int j = 0; j < p.K; ++j) total += __shfl(pb, j, 64);
-  const float score = p.norm ? round_bf16(pb / total) : pb;
-  if (lane < p.K) {
-    p.idx[t * p.K + lane] = my_sel;
-    p.scores[t * (p.K + 1) + lane] = score;
-    if (p.idx_out) p.idx_out[t * p.K + lane] = my_sel;
-    if (p.scores_out) p.scores_out[t * p.K + lane] = score;
+  for (int cb = 0; cb < 4; ++cb) wb[cb] = p.router_w + (size_t)(e0 + cb * 16 + col) * p.H + g * 16;
+  f32x4_r acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+  const int nch = p.H / 64;
+  for (int c0 = 0; c0 < nch; c0 += 4) {
+    u32x4 a[4][2], b[4][4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        a[u][j] = *reinterpret_cast<const u32x4*>(xa + (c0 + u) * 64 + 8 * j);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          b[u][cb][j] = *reinterpret_cast<const u32x4*>(wb[cb] + (c0 + u) * 64 + 8 * j);
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_r, a[u][j]), __builtin_bit_cast(bf16x8_r, b[u][cb][j]),
+              acc[cb], 0, 0, 0);
   }
-  if (lane == 0) {
-    float sg = 1.0f;
-    if (has_sg) sg = round_bf16(sigmoid(round_bf16(load_coherent(lg + p.E))));
-    p.scores[t * (p.K + 1) + p.K] = sg;
-    __hip_atomic_store(&p.ctr[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + 4 * g + i;
+      if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col] = acc[cb][i];
+    }
+}
+
+// The router contract's dot of one token row (held as xv, chunk lane + 64 c
+// per lane) with one weight row.
+template <int XC>
+__device__ __forceinline__ float contract_dot(const uint4 (&xv)[XC], int nxc,
+                                              const uint16_t* w) {
+  const int lane = threadIdx.x & 63;
+  uint4 wv[XC];
+#pragma unroll
+  for (int c = 0; c < XC; ++c)
+    if (c < nxc) wv[c] = load16(w + (lane + 64 * c) * 8);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < XC; ++c) {
+    if (c < nxc) {
+      acc = fmaf(bf16_lo(xv[c].x), bf16_lo(wv[c].x), acc);
+      acc = fmaf(bf16_hi(xv[c].x), bf16_hi(wv[c].x), acc);
+      acc = fmaf(bf16_lo(xv[c].y), bf16_lo(wv[c].y), acc);
+      acc = fmaf(bf16_hi(xv[c].y), bf16_hi(wv[c].y), acc);
+      acc = fmaf(bf16_lo(xv[c].z), bf16_lo(wv[c].z), acc);
+      acc = fmaf(bf16_hi(xv[c].z), bf16_hi(wv[c].z), acc);
+      acc = fmaf(bf16_lo(xv[c].w), bf16_lo(wv[c].w), acc);
+      acc = fmaf(bf16_hi(xv[c].w), bf16_hi(wv[c].w), acc);
+    }
   }
+  return wave_sum(acc);
+}
+
+__device__ __forceinline__ uint32_t f32_order_key(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float f32_from_order_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// One wave per token (E <= 256, H a multiple of 512 up to 4096).
+__global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
+                                                            const float* wnorm) {
+  constexpr int P = 4;
+  constexpr int XC = 8;
+  __shared__ uint32_t s_topk[4][128];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= p.T) return;
+  const float* lg = p.logits + (size_t)t * (p.E + 1);
+  const int nxc = p.H / 512;
+  uint4 xv[XC];
+  float nx2 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < XC; ++c) {
+    if (c < nxc) {
+      xv[c] = load16(p.x + (size_t)t * p.H + (lane + 64 * c) * 8);
+      const uint32_t vv[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nx2 = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), nx2);
+        nx2 = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), nx2);
+      }
+    }
+  }
+  const float nx = sqrtf(wave_sum(nx2)) * (1.0f + 1.0f / 1024.0f);
+  float lv[P], wn = 0.0f, amax = 0.0f;
+  uint32_t key[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int e = lane + 64 * i;
+    lv[i] = 0.0f;
+    key[i] = 0;
+    if (e < p.E) {
+      lv[i] = lg[e];
+      key[i] = f32_order_key(lv[i]);
+      wn = fmaxf(wn, wnorm[e]);
+      amax = fmaxf(amax, fabsf(lv[i]));
+    }
+  }
+  wn = __uint_as_float(wave_max_u32(__float_as_uint(wn)));      // non-negative
+  amax = __uint_as_float(wave_max_u32(__float_as_uint(amax)));
+  // k-th largest L (with multiplicity)
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) cnt += __popcll(__ballot(key[i] >= cand));
+    if (cnt >= p.K) thr = cand;
+  }
+  const float tk = f32_from_order_key(thr);
+  const float gam = (float)(p.H - 1) * 0x1p-23f + (float)(p.H / 64 + 8) * 0x1p-24f;
+  const float delta = gam * nx * wn + 0x1p-100f * (1.0f + nx + wn);
+  const float mag = amax + 2.0f * delta + 1.0f;
+  const int ex = (int)((__float_as_uint(mag) >> 23) & 0xFFu);
+  const float ulp = __uint_as_float((uint32_t)max(ex - 7, 1) << 23);
+  const float margin = (2.0f * delta + 1.25f * ulp) * (1.0f + 0x1p-20f);
+  const float lo = tk - margin;
+  float out[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) out[i] = lane + 64 * i < p.E ? round_bf16(lv[i]) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    uint64_t m = __ballot(lane + 64 * i < p.E && lv[i] >= lo);
+    while (m) {
+      const int bit = __ffsll((unsigned long long)m) - 1;
+      m &= m - 1;
+      const int e = bit + 64 * i;
+      const float c = contract_dot<XC>(xv, nxc, p.router_w + (size_t)e * p.H);
+      if (lane == bit) out[i] = round_bf16(c);
+    }
+  }
+  const bool has_sg = p.sgate_w != nullptr;
+  const float sg_logit = has_sg ? contract_dot<XC>(xv, nxc, p.sgate_w) : 0.0f;
+  finish_route<P>(p, t, out, sg_logit, s_topk[wave]);
 }
 
 // ----------------------------------------------------------------- gate/up
@@ -407,6 +623,20 @@ __global__ __launch_bounds__(256) void qmv_kernel(const QmvArgs p,
     hipError_t _e = hipGetLastError();       \
     if (_e != hipSuccess) return _e;         \
   } while (0)
+
+bool router_mfma_eligible(int E, int H) {
+  return E % 64 == 0 && E <= 256 && H % 512 == 0 && H <= 4096;
+}
+
+hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, hipStream_t s) {
+  hipLaunchKernelGGL(router_rownorm_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, wnorm);
+  hipLaunchKernelGGL(router_logits_mfma_kernel, dim3((a.T + 15) / 16, a.E / 64), dim3(64), 0,
+                     s, a);
+  hipLaunchKernelGGL(router_select_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                     (const float*)wnorm);
+  RMOE_CHECK_LAUNCH();
+  return hipSuccess;
+}
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
   const int rows = a.E + (a.sgate_w ? 1 : 0);

@@ -97,6 +97,9 @@ hipError_t fused_grid(int bits, int* grid);
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s);
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s);
+// Many-token router on the matrix cores with exact selection (prefill).
+bool router_mfma_eligible(int E, int H);
+hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, hipStream_t s);
 hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s);
 hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s);
 hipError_t launch_qmv(const QmvArgs& a, int bits, hipStream_t s);
@@ -111,12 +114,13 @@ hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* partials,
 
 // ---- prefill (prefill.hip): expert-sorted grouped dequant-GEMM on MFMA.
 constexpr int kPrefillMaxExperts = 512;  // buckets of the one-workgroup sort
-constexpr int kPrefillBM = 128;          // sorted rows per m-tile
+constexpr int kPrefillBM = 128;          // sorted rows per m-tile (long prefill)
 constexpr int kPrefillTileN = 128;       // [up; gate] pairs per gate/up tile
 constexpr int kPrefillMinRows = 64;      // (token, slot) rows that select it
 
 struct PrefillArgs {
   int T, H, I, E, K, has_shared;
+  int bm;                  // rows per m-tile (set by launch_prefill)
   const uint16_t* x;       // [T, H]
   const int32_t* idx;      // [T, K] expert ids (out of range -> zero rows)
   QW gu, dn, sgu, sdn;
@@ -130,7 +134,8 @@ struct PrefillArgs {
   uint16_t* out;           // [T, H]
 };
 
-int prefill_max_mtiles(int T, int K, int E);
+int prefill_tile_rows(int T, int K, int E);
+int prefill_max_mtiles(int T, int K, int E, int bm);
 hipError_t launch_prefill(const PrefillArgs& a, int bits, bool combine, hipStream_t s);
 
 }  // namespace rmoe

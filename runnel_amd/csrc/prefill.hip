@@ -49,20 +49,18 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kGemmThreads = 256;               // 4 waves
-constexpr int kBM = kPrefillBM;                 // rows per m-tile
-constexpr int kMB = kBM / 16;                   // MFMA row blocks per tile
-constexpr int kCB = kPrefillTileN / 64;         // 16-column blocks per wave
 constexpr int kDownTileN = 2 * kPrefillTileN;   // down columns per workgroup
 constexpr int kPad = 8;                         // bf16 of padding per LDS row
 
-template <int BITS>
+template <int BITS, int BM>
 struct Chunk {
   static constexpr int KC = BITS == 8 ? 64 : 128;      // k values per chunk
   static constexpr int NJ = KC / 32;                   // MFMAs per chunk
   static constexpr int WORDS = KC * BITS / 32;         // u32 per row per chunk
   static constexpr int ROW = KC + kPad;                // LDS row (bf16)
-  static constexpr int PIECES = kBM * KC / 8;          // 16-byte A pieces
+  static constexpr int PIECES = BM * KC / 8;           // 16-byte A pieces
   static constexpr int PPT = PIECES / kGemmThreads;    // pieces per thread
+  static_assert(PIECES % kGemmThreads == 0, "A tile must split evenly");
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -74,6 +72,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 template <int BITS>
 __device__ __forceinline__ bf16x8_t dequant_frag(const uint4 w, int j, float s, float b) {
   u32x4 d;
+
   if constexpr (BITS == 8) {
     const uint32_t w0 = j == 0 ? w.x : w.z;
     const uint32_t w1 = j == 0 ? w.y : w.w;
@@ -105,6 +104,7 @@ struct Tile {
   int n, bucket, row0, nrows;
 };
 
+template <int BM>
 __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& t) {
   const int NB = p.E + 2;
   const int MT = p.tile_offs[NB];
@@ -124,8 +124,8 @@ __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& 
     else hi = mid - 1;
   }
   t.bucket = lo;
-  t.row0 = p.offs[lo] + (rem - p.tile_offs[lo]) * kBM;
-  t.nrows = min(kBM, p.offs[lo + 1] - t.row0);
+  t.row0 = p.offs[lo] + (rem - p.tile_offs[lo]) * BM;
+  t.nrows = min(BM, p.offs[lo + 1] - t.row0);
   return true;
 }
 
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
     } else {
       for (int w = 0; w < kSortWaves; ++w) rows_b += s_hist[w * NB + tid];
     }
-    tiles_b = (rows_b + kBM - 1) / kBM;
+    tiles_b = (rows_b + p.bm - 1) / p.bm;
   }
   s_scan[0][tid] = rows_b;
   s_scan[1][tid] = tiles_b;
@@ -229,76 +229,83 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
   }
 }
 
-// ----------------------------------------------------------- gate/up GEMM
-template <int BITS>
-__global__ __launch_bounds__(kGemmThreads) void prefill_gate_up_kernel(const PrefillArgs p,
-                                                                        const int nt) {
-  using C = Chunk<BITS>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * C::ROW];
-  __shared__ int s_tok[kBM];
-  Tile tile;
-  if (!decode_tile(p, nt, tile)) return;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int I = p.I;
-  const int H = p.H;
-  const int TK = p.T * p.K;
-  const int col_l = lane & 15;
-  const int kg = lane >> 4;
+// ------------------------------------------------------------ grouped GEMM
+// MODE 0: gate/up.  A = x rows of the tile's tokens (K = H); the wave's four
+//         B column blocks are up rows c, c + 16 and gate rows I + c, I + c +
+//         16 of 32 pairs c; SwiGLU epilogue -> act[sorted row].
+// MODE 1: down.  A = act rows (contiguous in sorted order, K = I); B column
+//         blocks are 4 x 16 consecutive output columns; -> y[source row].
+// Rows of a partial tile are zero in LDS; only the 16-row blocks that hold
+// rows are multiplied (two specialisations: all blocks, or the first half).
+template <int BITS, int BM, int MODE>
+struct Gemm {
+  using C = Chunk<BITS, BM>;
+  static constexpr int MB = BM / 16;
+  static constexpr int TN = MODE == 0 ? kPrefillTileN : kDownTileN;
 
-  if (tile.bucket == p.E + 1) {
-    // out-of-range expert ids: zero activations, nothing loaded
-    for (int i = tid; i < tile.nrows * kPrefillTileN; i += kGemmThreads) {
-      const int r = i / kPrefillTileN;
-      const int c = tile.n * kPrefillTileN + (i - r * kPrefillTileN);
-      p.act[(size_t)(tile.row0 + r) * I + c] = 0;
-    }
-    return;
-  }
-  if (tid < kBM) {
-    int t = 0;
-    if (tid < tile.nrows) {
-      const int src = p.rows[tile.row0 + tid];
-      t = src < TK ? src / p.K : src - TK;
-    }
-    s_tok[tid] = t;
-  }
-  const bool shared = tile.bucket == p.E;
-  const QW q = shared ? p.sgu : p.gu;
-  const size_t e = shared ? 0 : (size_t)tile.bucket;
-  const int WPR = H * BITS / 32;
-  const int G = H / 64;
-  // this lane's up rows (c) and gate rows (I + c), one per column block
-  const uint32_t* wrow[kCB][2];
-  size_t prow[kCB][2];
-#pragma unroll
-  for (int cb = 0; cb < kCB; ++cb) {
-    const int c = tile.n * kPrefillTileN + wave * (16 * kCB) + cb * 16 + col_l;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      prow[cb][h] = e * 2 * I + (size_t)(c + h * I);
-      wrow[cb][h] = q.w + prow[cb][h] * WPR + kg * 4;
-    }
-  }
-  __syncthreads();  // s_tok
+  const PrefillArgs& p;
+  const Tile& tile;
+  uint16_t (*s_a)[BM * C::ROW];
+  const int* s_row;
+  int tid, wave, lane, col_l, kg, K;
+  QW q;
+  size_t brow[4];
+  const uint32_t* wptr[4];
 
-  const int nch = H / C::KC;
-  const int mb_active = (tile.nrows + 15) >> 4;
-  // A staging: piece i of the tile is row i / (KC / 8), 16-byte column i % (KC / 8)
-  uint4 ar[C::PPT];
-  auto load_a = [&](int ch) {
+  __device__ Gemm(const PrefillArgs& p_, const Tile& t_, uint16_t (*sa)[BM * C::ROW],
+                  const int* srow)
+      : p(p_), tile(t_), s_a(sa), s_row(srow) {
+    tid = threadIdx.x;
+    wave = tid >> 6;
+    lane = tid & 63;
+    col_l = lane & 15;
+    kg = lane >> 4;
+    const bool shared = tile.bucket == p.E;
+    const size_t e = shared ? 0 : (size_t)tile.bucket;
+    K = MODE == 0 ? p.H : p.I;
+    const int WPR = K * BITS / 32;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      if constexpr (MODE == 0) {
+        q = shared ? p.sgu : p.gu;
+        const int c = tile.n * TN + wave * 32 + (qq & 1) * 16 + col_l;
+        brow[qq] = e * 2 * p.I + (size_t)(c + (qq >> 1) * p.I);
+      } else {
+        q = shared ? p.sdn : p.dn;
+        const int c = tile.n * TN + wave * 64 + qq * 16 + col_l;
+        brow[qq] = e * p.H + (size_t)c;
+      }
+      wptr[qq] = q.w + brow[qq] * WPR + kg * 4;
+    }
+  }
+
+  // This thread's A pieces: row base pointers, fixed for the whole tile
+  // (null for rows past the tile's end).
+  __device__ __forceinline__ void a_rows(const uint16_t* (&src)[C::PPT]) const {
 #pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
       const int pi = tid + kGemmThreads * j;
       const int r = pi / (C::KC / 8);
       const int c8 = pi - r * (C::KC / 8);
-      ar[j] = make_uint4(0, 0, 0, 0);
-      if (r < tile.nrows)
-        ar[j] = load16(p.x + (size_t)s_tok[r] * H + ch * C::KC + c8 * 8);
+      src[j] = nullptr;
+      if (r < tile.nrows) {
+        if constexpr (MODE == 0)
+          src[j] = p.x + (size_t)s_row[r] * p.H + c8 * 8;
+        else
+          src[j] = p.act + (size_t)(tile.row0 + r) * p.I + c8 * 8;
+      }
     }
-  };
-  auto store_a = [&](int buf) {
+  }
+
+  __device__ __forceinline__ void load_a(int ch, const uint16_t* const (&src)[C::PPT],
+                                         uint4 (&ar)[C::PPT]) const {
+#pragma unroll
+    for (int j = 0; j < C::PPT; ++j) {
+      ar[j] = make_uint4(0, 0, 0, 0);
+      if (src[j]) ar[j] = load16(src[j] + ch * C::KC);
+    }
+  }
+  __device__ __forceinline__ void store_a(int buf, const uint4 (&ar)[C::PPT]) const {
 #pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
       const int pi = tid + kGemmThreads * j;
@@ -306,256 +313,190 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gate_up_kernel(const Pre
       const int c8 = pi - r * (C::KC / 8);
       *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) = ar[j];
     }
-  };
-  uint4 bw[kCB][2];
-  float bs[kCB][2], bb[kCB][2];
-  auto load_b = [&](int ch, uint4 (&w)[kCB][2], float (&s)[kCB][2], float (&b)[kCB][2]) {
+  }
+  // Scales and biases stay raw bf16 bits until the chunk that uses them, so
+  // a prefetch is never waited for where it is issued.
+  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[4], uint32_t (&s)[4],
+                                         uint32_t (&b)[4]) const {
+    const int G = K / 64;
     const int g = BITS == 8 ? ch : 2 * ch + (kg >> 1);
 #pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        s[cb][h] = bf16_to_f32(q.s[prow[cb][h] * G + g]);
-        b[cb][h] = bf16_to_f32(q.b[prow[cb][h] * G + g]);
-      }
-#pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) w[cb][h] = load16_stream(wrow[cb][h] + ch * C::WORDS);
-  };
-
-  f32x4_t acc[kMB][kCB][2];
-#pragma unroll
-  for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) acc[mb][cb][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  load_b(0, bw, bs, bb);
-  load_a(0);
-  store_a(0);
-  __syncthreads();
-  for (int ch = 0; ch < nch; ++ch) {
-    const int buf = ch & 1;
-    uint4 nw[kCB][2];
-    float ns[kCB][2], nb[kCB][2];
-    const bool more = ch + 1 < nch;
-    if (more) {
-      load_b(ch + 1, nw, ns, nb);
-      load_a(ch + 1);
+    for (int qq = 0; qq < 4; ++qq) {
+      s[qq] = q.s[brow[qq] * G + g];
+      b[qq] = q.b[brow[qq] * G + g];
     }
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) w[qq] = load16_stream(wptr[qq] + ch * C::WORDS);
+  }
+
+  // One chunk of KC: NJ MFMA steps over the first MBA row blocks.  The LDS
+  // reads and the dequantisation of step j + 1 are interleaved with the
+  // MFMAs of step j, so the matrix core, the vector ALU and the LDS of the
+  // SIMD work at the same time.
+  template <int MBA>
+  __device__ __forceinline__ void chunk(int buf, const uint4 (&w)[4], const uint32_t (&sraw)[4],
+                                        const uint32_t (&braw)[4], f32x4_t (&acc)[MB][4]) const {
     const uint16_t* sa = &s_a[buf][col_l * C::ROW + kg * (C::KC / 4)];
+    float s[4], b[4];
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      s[qq] = bf16_to_f32(sraw[qq]);
+      b[qq] = bf16_to_f32(braw[qq]);
+    }
+    auto read_a = [&](int j, bf16x8_t (&a)[MBA]) {
+#pragma unroll
+      for (int mb = 0; mb < MBA; ++mb)
+        a[mb] = __builtin_bit_cast(
+            bf16x8_t, *reinterpret_cast<const u32x4*>(sa + mb * 16 * C::ROW + 8 * j));
+    };
+    bf16x8_t a[MBA], bf[4];
+    read_a(0, a);
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) bf[qq] = dequant_frag<BITS>(w[qq], 0, s[qq], b[qq]);
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
-      bf16x8_t bf[kCB][2];
+      bf16x8_t na[MBA], nbf[4];
+      if (j + 1 < C::NJ) {
+        read_a(j + 1, na);
 #pragma unroll
-      for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          bf[cb][h] = dequant_frag<BITS>(bw[cb][h], j, bs[cb][h], bb[cb][h]);
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) {
-        if (mb < mb_active) {
-          const bf16x8_t a = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const u32x4*>(sa + mb * 16 * C::ROW + 8 * j));
-#pragma unroll
-          for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) acc[mb][cb][h] = mfma(a, bf[cb][h], acc[mb][cb][h]);
-        }
+        for (int qq = 0; qq < 4; ++qq) nbf[qq] = dequant_frag<BITS>(w[qq], j + 1, s[qq], b[qq]);
       }
-    }
-    if (more) store_a(buf ^ 1);
-    __syncthreads();
-    if (more) {
 #pragma unroll
-      for (int cb = 0; cb < kCB; ++cb)
+      for (int mb = 0; mb < MBA; ++mb)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          bw[cb][h] = nw[cb][h];
-          bs[cb][h] = ns[cb][h];
-          bb[cb][h] = nb[cb][h];
+        for (int qq = 0; qq < 4; ++qq) acc[mb][qq] = mfma(a[mb], bf[qq], acc[mb][qq]);
+      if (j + 1 < C::NJ) {
+        // per MFMA: one MFMA, a share of the next step's LDS reads and of
+        // its dequantisation
+        constexpr int kValuPer = (BITS == 8 ? 80 : 112) / (4 * MBA) + 1;
+#pragma unroll
+        for (int i = 0; i < 4 * MBA; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (i % 4 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
         }
+#pragma unroll
+        for (int mb = 0; mb < MBA; ++mb) a[mb] = na[mb];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) bf[qq] = nbf[qq];
+      }
     }
   }
 
-  // SwiGLU epilogue: up and gate of one pair sit in the same lane/register
+  template <int MBA>
+  __device__ void run(f32x4_t (&acc)[MB][4]) const {
+    const int nch = K / C::KC;
+    const uint16_t* asrc[C::PPT];
+    a_rows(asrc);
+    uint4 ar[C::PPT];
+    uint4 bw[4];
+    uint32_t bs[4], bb[4];
+    load_b(0, bw, bs, bb);
+    load_a(0, asrc, ar);
+    store_a(0, ar);
+    __syncthreads();
+    for (int ch = 0; ch < nch; ++ch) {
+      const int buf = ch & 1;
+      // the prefetch is unconditional (the last chunk loads itself again)
+      // so no branch splits the loop body
+      const int nx = min(ch + 1, nch - 1);
+      uint4 nw[4];
+      uint32_t ns[4], nb[4];
+      load_b(nx, nw, ns, nb);
+      load_a(nx, asrc, ar);
+      chunk<MBA>(buf, bw, bs, bb, acc);
+      store_a(buf ^ 1, ar);
+      __syncthreads();
 #pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) {
-    if (mb >= mb_active) continue;
+      for (int qq = 0; qq < 4; ++qq) {
+        bw[qq] = nw[qq];
+        bs[qq] = ns[qq];
+        bb[qq] = nb[qq];
+      }
+    }
+  }
+
+  __device__ void epilogue(const f32x4_t (&acc)[MB][4], int mba) const {
 #pragma unroll
-    for (int cb = 0; cb < kCB; ++cb) {
-      const int c = tile.n * kPrefillTileN + wave * (16 * kCB) + cb * 16 + col_l;
+    for (int mb = 0; mb < MB; ++mb) {
+      if (mb >= mba) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = mb * 16 + kg * 4 + i;
-        if (r < tile.nrows) {
-          const float up = round_bf16(acc[mb][cb][0][i]);
-          const float gate = round_bf16(acc[mb][cb][1][i]);
-          p.act[(size_t)(tile.row0 + r) * I + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
+        if (r >= tile.nrows) continue;
+        if constexpr (MODE == 0) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int c = tile.n * TN + wave * 32 + h * 16 + col_l;
+            const float up = round_bf16(acc[mb][h][i]);
+            const float gate = round_bf16(acc[mb][2 + h][i]);
+            p.act[(size_t)(tile.row0 + r) * p.I + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
+          }
+        } else {
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            const int c = tile.n * TN + wave * 64 + qq * 16 + col_l;
+            p.y[(size_t)s_row[r] * p.H + c] = (uint16_t)f32_to_bf16(acc[mb][qq][i]);
+          }
         }
       }
     }
   }
-}
+};
 
-// -------------------------------------------------------------- down GEMM
-template <int BITS>
-__global__ __launch_bounds__(kGemmThreads) void prefill_down_kernel(const PrefillArgs p,
+template <int BITS, int BM, int MODE>
+__global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(const PrefillArgs p,
                                                                      const int nt) {
-  using C = Chunk<BITS>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * C::ROW];
-  __shared__ int s_dst[kBM];
+  using G = Gemm<BITS, BM, MODE>;
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * G::C::ROW];
+  __shared__ int s_row[BM];
   Tile tile;
-  if (!decode_tile(p, nt, tile)) return;
+  if (!decode_tile<BM>(p, nt, tile)) return;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int I = p.I;
-  const int H = p.H;
-  const int col_l = lane & 15;
-  const int kg = lane >> 4;
-  if (tid < kBM) s_dst[tid] = tid < tile.nrows ? p.rows[tile.row0 + tid] : 0;
+  const int TK = p.T * p.K;
+  if (tid < BM) {
+    int v = 0;
+    if (tid < tile.nrows) {
+      const int src = p.rows[tile.row0 + tid];
+      // gate/up: the token of the row; down: where its output goes
+      v = MODE == 0 ? (src < TK ? src / p.K : src - TK) : src;
+    }
+    s_row[tid] = v;
+  }
   __syncthreads();
-
   if (tile.bucket == p.E + 1) {
-    for (int i = tid; i < tile.nrows * kDownTileN; i += kGemmThreads) {
-      const int r = i / kDownTileN;
-      const int c = tile.n * kDownTileN + (i - r * kDownTileN);
-      p.y[(size_t)s_dst[r] * H + c] = 0;
+    // out-of-range expert ids: zero rows, nothing loaded
+    for (int i = tid; i < tile.nrows * G::TN; i += kGemmThreads) {
+      const int r = i / G::TN;
+      const int c = tile.n * G::TN + (i - r * G::TN);
+      if constexpr (MODE == 0)
+        p.act[(size_t)(tile.row0 + r) * p.I + c] = 0;
+      else
+        p.y[(size_t)s_row[r] * p.H + c] = 0;
     }
     return;
   }
-  const bool shared = tile.bucket == p.E;
-  const QW q = shared ? p.sdn : p.dn;
-  const size_t e = shared ? 0 : (size_t)tile.bucket;
-  const int WPR = I * BITS / 32;
-  const int G = I / 64;
-  const uint32_t* wrow[kCB][2];
-  size_t prow[kCB][2];
-  // the down tile's 256 output columns: wave w owns 64, as 2 x kCB
-  // 16-column MFMA tiles
+  const G g(p, tile, s_a, s_row);
+  f32x4_t acc[G::MB][4];
 #pragma unroll
-  for (int cb = 0; cb < kCB; ++cb)
+  for (int mb = 0; mb < G::MB; ++mb)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = tile.n * kDownTileN + wave * 64 + h * 16 * kCB + cb * 16 + col_l;
-      prow[cb][h] = e * H + (size_t)c;
-      wrow[cb][h] = q.w + prow[cb][h] * WPR + kg * 4;
+    for (int qq = 0; qq < 4; ++qq) acc[mb][qq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int mba = (tile.nrows + 15) >> 4;
+  if (mba > G::MB / 2) {
+    g.template run<G::MB>(acc);
+    g.epilogue(acc, G::MB);
+  } else if constexpr (G::MB >= 4) {
+    if (mba > G::MB / 4) {
+      g.template run<G::MB / 2>(acc);
+      g.epilogue(acc, G::MB / 2);
+    } else {
+      g.template run<G::MB / 4>(acc);
+      g.epilogue(acc, G::MB / 4);
     }
-
-  const int nch = I / C::KC;
-  const int mb_active = (tile.nrows + 15) >> 4;
-  uint4 ar[C::PPT];
-  auto load_a = [&](int ch) {
-#pragma unroll
-    for (int j = 0; j < C::PPT; ++j) {
-      const int pi = tid + kGemmThreads * j;
-      const int r = pi / (C::KC / 8);
-      const int c8 = pi - r * (C::KC / 8);
-      ar[j] = make_uint4(0, 0, 0, 0);
-      if (r < tile.nrows)
-        ar[j] = load16(p.act + (size_t)(tile.row0 + r) * I + ch * C::KC + c8 * 8);
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < C::PPT; ++j) {
-      const int pi = tid + kGemmThreads * j;
-      const int r = pi / (C::KC / 8);
-      const int c8 = pi - r * (C::KC / 8);
-      *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) = ar[j];
-    }
-  };
-  uint4 bw[kCB][2];
-  float bs[kCB][2], bb[kCB][2];
-  auto load_b = [&](int ch, uint4 (&w)[kCB][2], float (&s)[kCB][2], float (&b)[kCB][2]) {
-    const int g = BITS == 8 ? ch : 2 * ch + (kg >> 1);
-#pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        s[cb][h] = bf16_to_f32(q.s[prow[cb][h] * G + g]);
-        b[cb][h] = bf16_to_f32(q.b[prow[cb][h] * G + g]);
-      }
-#pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) w[cb][h] = load16_stream(wrow[cb][h] + ch * C::WORDS);
-  };
-
-  f32x4_t acc[kMB][kCB][2];
-#pragma unroll
-  for (int mb = 0; mb < kMB; ++mb)
-#pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) acc[mb][cb][h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  load_b(0, bw, bs, bb);
-  load_a(0);
-  store_a(0);
-  __syncthreads();
-  for (int ch = 0; ch < nch; ++ch) {
-    const int buf = ch & 1;
-    uint4 nw[kCB][2];
-    float ns[kCB][2], nb[kCB][2];
-    const bool more = ch + 1 < nch;
-    if (more) {
-      load_b(ch + 1, nw, ns, nb);
-      load_a(ch + 1);
-    }
-    const uint16_t* sa = &s_a[buf][col_l * C::ROW + kg * (C::KC / 4)];
-#pragma unroll
-    for (int j = 0; j < C::NJ; ++j) {
-      bf16x8_t bf[kCB][2];
-#pragma unroll
-      for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          bf[cb][h] = dequant_frag<BITS>(bw[cb][h], j, bs[cb][h], bb[cb][h]);
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) {
-        if (mb < mb_active) {
-          const bf16x8_t a = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const u32x4*>(sa + mb * 16 * C::ROW + 8 * j));
-#pragma unroll
-          for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) acc[mb][cb][h] = mfma(a, bf[cb][h], acc[mb][cb][h]);
-        }
-      }
-    }
-    if (more) store_a(buf ^ 1);
-    __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          bw[cb][h] = nw[cb][h];
-          bs[cb][h] = ns[cb][h];
-          bb[cb][h] = nb[cb][h];
-        }
-    }
-  }
-
-#pragma unroll
-  for (int mb = 0; mb < kMB; ++mb) {
-    if (mb >= mb_active) continue;
-#pragma unroll
-    for (int cb = 0; cb < kCB; ++cb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int c = tile.n * kDownTileN + wave * 64 + h * 16 * kCB + cb * 16 + col_l;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = mb * 16 + kg * 4 + i;
-          if (r < tile.nrows)
-            p.y[(size_t)s_dst[r] * H + c] = (uint16_t)f32_to_bf16(acc[mb][cb][h][i]);
-        }
-      }
+  } else {
+    g.template run<G::MB / 2>(acc);
+    g.epilogue(acc, G::MB / 2);
   }
 }
 
@@ -607,23 +548,40 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs 
 }
 
 // --------------------------------------------------------------- launchers
-int prefill_max_mtiles(int T, int K, int E) {
-  return (T * K + T + kBM - 1) / kBM + E + 2;
+int prefill_tile_rows(int T, int K, int E) {
+  // few rows per expert (a short prefill chunk): 32-row tiles keep the
+  // wasted MFMA rows low; otherwise 128-row tiles share each dequantised
+  // weight fragment across more rows
+  return (long)T * K <= 48L * E ? 32 : kPrefillBM;
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, int bits, bool combine, hipStream_t s) {
-  hipLaunchKernelGGL(prefill_sort_kernel, dim3(1), dim3(kSortThreads), 0, s, a);
-  const int mt = prefill_max_mtiles(a.T, a.K, a.E);
+int prefill_max_mtiles(int T, int K, int E, int bm) {
+  return (T * K + T + bm - 1) / bm + E + 2;
+}
+
+template <int BITS, int BM>
+void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
   const int nt_gu = a.I / kPrefillTileN;
   const int nt_dn = a.H / kDownTileN;
   const int g_gu = 8 * ((nt_gu * mt + 7) / 8);
   const int g_dn = 8 * ((nt_dn * mt + 7) / 8);
+  hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu), dim3(kGemmThreads), 0, s,
+                     a, nt_gu);
+  hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn), dim3(kGemmThreads), 0, s,
+                     a, nt_dn);
+}
+
+hipError_t launch_prefill(const PrefillArgs& args, int bits, bool combine, hipStream_t s) {
+  PrefillArgs a = args;
+  a.bm = prefill_tile_rows(a.T, a.K, a.E);
+  hipLaunchKernelGGL(prefill_sort_kernel, dim3(1), dim3(kSortThreads), 0, s, a);
+  const int mt = prefill_max_mtiles(a.T, a.K, a.E, a.bm);
   if (bits == 8) {
-    hipLaunchKernelGGL(prefill_gate_up_kernel<8>, dim3(g_gu), dim3(kGemmThreads), 0, s, a, nt_gu);
-    hipLaunchKernelGGL(prefill_down_kernel<8>, dim3(g_dn), dim3(kGemmThreads), 0, s, a, nt_dn);
+    if (a.bm == 32) launch_gemms<8, 32>(a, mt, s);
+    else launch_gemms<8, kPrefillBM>(a, mt, s);
   } else {
-    hipLaunchKernelGGL(prefill_gate_up_kernel<4>, dim3(g_gu), dim3(kGemmThreads), 0, s, a, nt_gu);
-    hipLaunchKernelGGL(prefill_down_kernel<4>, dim3(g_dn), dim3(kGemmThreads), 0, s, a, nt_dn);
+    if (a.bm == 32) launch_gemms<4, 32>(a, mt, s);
+    else launch_gemms<4, kPrefillBM>(a, mt, s);
   }
   if (combine) hipLaunchKernelGGL(prefill_combine_kernel, dim3(a.T), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -87,3 +87,32 @@ def make_x(seed: int, tokens: int, hidden: int, device="cuda") -> torch.Tensor:
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     return torch.randn((tokens, hidden), generator=gen, device=device).to(BF16)
+
+
+# Skewed routing for long prefill: a per-expert router logit bias
+# -alpha * s * ln(rank) (Zipf exponent s) over a seeded random ranking of the
+# experts.  The block has no router bias term, so the bias rides on one input
+# feature held constant: x[:, 0] = BIAS_FEATURE for every token and router
+# column 0 = bias / BIAS_FEATURE.  With alpha 0.8 and s 1.1, 8192 tokens at
+# top-8 of 256 give about 16 experts more than 1000 rows each while about
+# half the experts receive fewer than 8.
+BIAS_FEATURE = 4.0
+
+
+def zipf_bias(seed: int, experts: int, s: float = 1.1, alpha: float = 0.8,
+              device="cuda") -> torch.Tensor:
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(seed)
+    rank = torch.randperm(experts, generator=gen).to(torch.float64) + 1.0
+    return (-alpha * s * torch.log(rank)).to(torch.float32).to(device)
+
+
+def apply_router_bias(layer: LayerWeights, bias: torch.Tensor) -> None:
+    """Route `bias` through input feature 0 (inputs from make_skewed_x)."""
+    layer.router_w[:, 0] = (bias / BIAS_FEATURE).to(BF16)
+
+
+def make_skewed_x(seed: int, tokens: int, hidden: int, device="cuda") -> torch.Tensor:
+    x = make_x(seed, tokens, hidden, device)
+    x[:, 0] = BIAS_FEATURE
+    return x

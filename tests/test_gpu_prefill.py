@@ -123,3 +123,69 @@ def test_block_prefill_512_tokens_8bit(torch_cuda):
     mx_ = M.bf16_to_f32(mlx)
     assert np.abs(got - mx_).max() <= MAX_ABS
     assert cosine(got.reshape(-1), mx_.reshape(-1)) >= MIN_COS
+
+
+@pytest.mark.parametrize("shape", [dict(hidden=1024, experts=128, top_k=8),
+                                   dict(hidden=512, experts=64, top_k=6)])
+def test_matrix_core_router_selection_is_exact(torch_cuda, shape):
+    """Many tokens route through the MFMA logits + exact re-check path:
+    indices equal the oracle's bit for bit, scores within a bf16 step."""
+    import torch
+    from runnel_amd import native
+    L = M.make_layer(77, inter=128, bits=8, **shape)
+    x = M.make_x(78, 200, shape["hidden"])
+    h = layer_to_dev(L)
+    out, idx, scores = native.moe_block(h, dev_bf16(x), return_routing=True)
+    torch.cuda.synchronize()
+    ref_idx, ref_scores, _ = M.route(x, L.router_w, L.top_k)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    assert np.abs(scores.cpu().numpy() - ref_scores).max() <= 2.0 ** -8
+    ref, _, _ = M.block_forward(L, x, mode="prefill")
+    got = M.bf16_to_f32(host_bf16(out))
+    assert _mismatches(got, M.bf16_to_f32(ref)) <= got.size // 500
+
+
+def test_matrix_core_router_ties_break_by_index(torch_cuda):
+    """Pairs of identical router rows give exactly tied logits; the lower
+    expert index must win each tie, as in the oracle."""
+    import torch
+    from runnel_amd import native
+    L = M.make_layer(79, hidden=512, inter=128, experts=64, top_k=5, bits=8)
+    L.router_w[1::2] = L.router_w[0::2]
+    x = M.make_x(80, 96, 512)
+    h = layer_to_dev(L)
+    _, idx, _ = native.moe_block(h, dev_bf16(x), return_routing=True)
+    torch.cuda.synchronize()
+    ref_idx, _, logits = M.route(x, L.router_w, L.top_k)
+    assert M.boundary_ties(logits, L.top_k).any()
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+
+
+def test_long_prefill_skewed_routing_4bit(torch_cuda):
+    """The long prefill workload: 8192 tokens, full-size 4-bit layer, router
+    biased by a Zipf(1.1) ranking (some experts over 1000 rows, many under
+    8).  Routing is checked bit-exact on 256 sampled tokens and outputs on 48
+    (a token's routing and output depend on that token only)."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lw = synthetic.make_layer(5150, bits=4)
+    synthetic.apply_router_bias(lw, synthetic.zipf_bias(5150, 256))
+    x = synthetic.make_skewed_x(5151, 8192, 2048)
+    h = lw.handle()
+    out, idx, _ = native.moe_block(h, x, return_routing=True)
+    torch.cuda.synchronize()
+    counts = np.bincount(idx.cpu().numpy().reshape(-1), minlength=256)
+    assert counts.max() > 1000 and (counts < 8).sum() > 64
+    L = layer_from_dev(lw)
+    xb = host_bf16(x)
+    sample = np.random.default_rng(0).choice(8192, 256, replace=False)
+    ref_idx, _, _ = M.route(xb[sample], L.router_w, 8)
+    assert np.array_equal(idx.cpu().numpy()[sample], ref_idx)
+    few = sample[:48]
+    ref, _, _ = M.block_forward(L, xb[few], mode="prefill")
+    got = M.bf16_to_f32(host_bf16(out))[few]
+    assert _mismatches(got, M.bf16_to_f32(ref)) <= got.size // 500
+    mlx, _, _ = M.block_forward(L, xb[few], mode="mlx")
+    mx_ = M.bf16_to_f32(mlx)
+    assert np.abs(got - mx_).max() <= MAX_ABS
+    assert cosine(got.reshape(-1), mx_.reshape(-1)) >= MIN_COS
