@@ -37,6 +37,11 @@ namespace {
 constexpr int kThreads = kFusedThreads;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSpinLimit = 1 << 20;
+// Waves that collect the hand-overs for their workgroup: router rows and
+// shared-expert pairs (prefetched for the next layer) sit on waves 0 and 1.
+constexpr int kPollWave = kWaves - 1;  // logits
+constexpr int kXPollWaves = 4;         // x: waves 4..7
+constexpr int kActPollWaves = 6;       // act: waves 2..7
 
 __device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -72,6 +77,74 @@ __device__ __forceinline__ uint32_t wave_max_fast(uint32_t v) {
   const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
   return a > b ? a : b;
 }
+// One wave collects n_words tagged words written by other workgroups: 16-byte
+// loads at agent coherence (sc1, the bits agent-scope atomic loads use; each
+// 4-byte word is as one store left it), repeated only for the pieces whose
+// tags are not yet current, and the values (bf16 in the high half) go to
+// LDS as floats.  Polling from one wave that has no prefetch outstanding
+// keeps each round trip short (a wave's loads return in order) and the
+// polling traffic to one stream per workgroup.
+template <int NL>
+__device__ __forceinline__ void poll_tagged(const uint32_t* src, int n_words, uint32_t tag,
+                                            float* dst, int lane, int part, bool& timed_out) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(src), (short)0, n_words * 4, 0x00020000);
+  // this wave's pieces: j0 + j, j < NL (16 bytes per lane each)
+  const int j0 = part * NL;
+  uint32_t pend = 0;
+#pragma unroll
+  for (int j = 0; j < NL; ++j)
+    if ((lane + 64 * (j0 + j)) * 4 < n_words) pend |= 1u << j;
+  for (int spin = 0;; ++spin) {
+    u32x4 v[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      if ((pend >> j) & 1u)
+        v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (lane + 64 * (j0 + j)) * 16, 0, 16);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      if ((pend >> j) & 1u) {
+        if (tag_ok(v[j].x, tag) && tag_ok(v[j].y, tag) && tag_ok(v[j].z, tag) &&
+            tag_ok(v[j].w, tag)) {
+          *reinterpret_cast<float4*>(dst + (lane + 64 * (j0 + j)) * 4) =
+              make_float4(__uint_as_float(v[j].x & 0xFFFF0000u),
+                          __uint_as_float(v[j].y & 0xFFFF0000u),
+                          __uint_as_float(v[j].z & 0xFFFF0000u),
+                          __uint_as_float(v[j].w & 0xFFFF0000u));
+          pend &= ~(1u << j);
+        }
+      }
+    }
+    if (!__any(pend != 0u)) break;
+    if (spin >= kSpinLimit) {
+      timed_out = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// wave_sum of N values at once, level by level (the same operations per
+// value as wave_sum, so the same results; the N chains overlap).
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0xB1);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x4E);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x141);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x140);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[i]), 0x401F));
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 32));
+}
+
 __device__ __forceinline__ void cswap_desc(uint32_t& a, uint32_t& b) {
   const uint32_t hi = a > b ? a : b;
   const uint32_t lo = a > b ? b : a;
@@ -170,38 +243,47 @@ __device__ __forceinline__ void issue_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Routing-independent loads of one layer for this wave: its router row and,
-// for the shared expert (unit K), its gate/up pairs and its down row.  For
-// a chained layer they are issued while the previous layer finishes.
-template <int BITS, int CPL, int NP, int RC>
-__device__ __forceinline__ void issue_prologue(const FusedLayer& L, int row, int n_rows, int E,
-                                               bool has_shared, int K, int gwave, int n_waves,
-                                               int n_pairs, int h, int lane, uint4 (&rw)[RC],
-                                               PairRegs<CPL> (&pr)[NP],
-                                               DownRegs<Shape<BITS>::DN_WPL>& drs,
-                                               uint32_t& dpws) {
+// Routing-independent loads of one layer for this wave, in two parts: its
+// router row and its down row of the shared expert (needed first), and its
+// gate/up pairs of the shared expert (unit K).  For a chained layer the
+// first part is issued right after the current layer's routed loads and
+// the second after the current layer's down projection, so neither delays
+// a hand-over.
+template <int BITS, int RC>
+__device__ __forceinline__ void issue_router_and_shared_down(
+    const FusedLayer& L, int row, int n_rows, int E, bool has_shared, int h, int lane,
+    uint4 (&rw)[RC], DownRegs<Shape<BITS>::DN_WPL>& drs, uint32_t& dpws) {
   using S = Shape<BITS>;
-  constexpr int I = S::I;
   constexpr int H = S::H;
   if (row < n_rows) {
     const uint16_t* wr = row < E ? L.router_w + (size_t)row * H : L.sgate_w;
 #pragma unroll
     for (int i = 0; i < RC; ++i) rw[i] = load16_stream(wr + (lane + 64 * i) * 8);
   }
+  if (has_shared && h < H) {
+    if (lane < 8) dpws = load_down_param_word<BITS>(L.sdn, h, lane);
+    load_down_words<BITS>(drs, L.sdn, h, lane);
+  }
+  issue_fence();
+}
+
+template <int BITS, int CPL, int NP>
+__device__ __forceinline__ void issue_shared_pairs(const FusedLayer& L, bool has_shared, int K,
+                                                   int pw, int n_waves, int n_pairs, int lane,
+                                                   PairRegs<CPL> (&pr)[NP]) {
+  constexpr int I = Shape<BITS>::I;
   if (has_shared) {
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-      const int q = gwave + pp * n_waves;
+      const int q = pw + pp * n_waves;
       if (q < n_pairs && q / I == K) load_pair_params<BITS, CPL>(pr[pp], L.sgu, q - K * I, lane);
     }
-    if (h < H && lane < 8) dpws = load_down_param_word<BITS>(L.sdn, h, lane);
     issue_fence();
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-      const int q = gwave + pp * n_waves;
+      const int q = pw + pp * n_waves;
       if (q < n_pairs && q / I == K) load_pair_words<BITS, CPL>(pr[pp], L.sgu, q - K * I, lane);
     }
-    if (h < H) load_down_words<BITS>(drs, L.sdn, h, lane);
   }
   issue_fence();
 }
@@ -216,10 +298,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   constexpr int NP = kMaxFusedPairsPerWave;
   constexpr int NU = kMaxFusedUnits;
   constexpr int kStageX = H / kThreads;                     // 4
-  constexpr int kStageAct = NU * I / kThreads;              // 9
   constexpr int kPer = kFusedMaxExperts / 64;               // keys per lane (4)
   constexpr int RC = H / 8 / 64;                            // router chunks per lane
   static_assert(kPer == 4, "the local sort network below is for 4 keys per lane");
+  static_assert(H % (256 * kXPollWaves) == 0 && NU * I % (256 * kActPollWaves) == 0,
+                "hand-overs split evenly over the polling waves");
   const int G = gridDim.x;
   const int wg = blockIdx.x;
   const int wave = threadIdx.x >> 6;
@@ -232,6 +315,9 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   const int n_pairs = U * I;
   const int h = gwave;            // one down row per wave (n_waves >= H is checked)
   const int row = wg + G * wave;  // router row of this wave, if any
+  // gate/up pairs q = pw + pp * n_waves: the pairs past 2 * n_waves land on
+  // low wave indices of every workgroup, so each CU streams the same bytes
+  const int pw = wg + G * wave;
   FusedScratch* sc = p.scratch;
 
   __shared__ float s_x[H];
@@ -249,14 +335,14 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 
   PairRegs<CPL> pr[NP];
   DownRegs<S::DN_WPL> dr[NU];      // slot NU-1: the shared unit
-  DownRegs<S::DN_WPL> dr_next;     // the next layer's shared down row
-  uint32_t dpw0 = 0, dpw1 = 0, dpw1_next = 0;
+  uint32_t dpw0 = 0, dpw1 = 0;
   uint4 rw[RC];
   {
     const FusedLayer L0 = p.table ? p.table[0] : p.layer0;
     const int n_rows0 = E + ((p.has_shared && L0.sgate_w) ? 1 : 0);
-    issue_prologue<BITS, CPL, NP, RC>(L0, row, n_rows0, E, p.has_shared, K, gwave, n_waves,
-                                      n_pairs, h, lane0, rw, pr, dr[NU - 1], dpw1);
+    issue_router_and_shared_down<BITS, RC>(L0, row, n_rows0, E, p.has_shared, h, lane0, rw,
+                                           dr[NU - 1], dpw1);
+    issue_shared_pairs<BITS, CPL, NP>(L0, p.has_shared, K, pw, n_waves, n_pairs, lane0, pr);
   }
   __syncthreads();
   const uint32_t base = s_base;
@@ -279,27 +365,15 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     const bool sg_row = p.has_shared && L.sgate_w;
     const int n_rows = E + (sg_row ? 1 : 0);
 
-    // ---- x (bf16 -> fp32 in LDS).  A chained layer polls the previous
+    // ---- x (bf16 -> fp32 in LDS).  A chained layer collects the previous
     // layer's tagged output.
-    {
-      if (!first) {
-        const uint32_t* src = sc->xs[(layer - 1) & 1];
-        const uint32_t want = tag_logit - 1;  // the previous layer's tag_x
-        for (int spin = 0;; ++spin) {
-          bool ok = true;
-#pragma unroll
-          for (int j = 0; j < kStageX; ++j) {
-            xin[j] = load_coherent_u32(src + threadIdx.x + j * kThreads);
-            ok &= tag_ok(xin[j], want);
-          }
-          if (ok) break;
-          if (spin >= kSpinLimit) { timed_out = true; break; }
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
+    if (first) {
 #pragma unroll
       for (int j = 0; j < kStageX; ++j)
         s_x[threadIdx.x + j * kThreads] = __uint_as_float(xin[j] & 0xFFFF0000u);
+    } else if (wave >= kWaves - kXPollWaves) {
+      poll_tagged<H / 256 / kXPollWaves>(sc->xs[(layer - 1) & 1], H, tag_logit - 1, s_x, lane,
+                                         wave - (kWaves - kXPollWaves), timed_out);
     }
     __syncthreads();
 
@@ -323,17 +397,21 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     }
 
     // ---- K: poll all logits (wave 0), rank them, publish in LDS.
-    if (wave == 0) {
+    if (wave == kPollWave) {
+      // lane l holds experts 4 l .. 4 l + 3 (one 16-byte coherent load)
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          sc->logits, (short)0, (E + 1) * 4, 0x00020000);
       uint32_t w[kPer];
       uint32_t wsg = 0;
       for (int spin = 0;; ++spin) {
         bool ok = true;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, 0, 16);
+        w[0] = v.x;
+        w[1] = v.y;
+        w[2] = v.z;
+        w[3] = v.w;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-          const int e = lane + 64 * i;
-          w[i] = e < E ? load_coherent_u32(sc->logits + e) : 0u;
-          ok &= e >= E || tag_ok(w[i], tag_logit);
-        }
+        for (int i = 0; i < kPer; ++i) ok &= 4 * lane + i >= E || tag_ok(w[i], tag_logit);
         if (sg_row && lane == 0) {
           wsg = load_coherent_u32(sc->logits + E);
           ok &= tag_ok(wsg, tag_logit);
@@ -346,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       float lv[kPer];
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
-        const int e = lane + 64 * i;
+        const int e = 4 * lane + i;
         const uint32_t b = w[i] >> 16;
         lv[i] = bf16_to_f32(b);
         k[i] = e < E ? ((bf16_order_key(b) << 16) | (0xFFFFu - (uint32_t)e)) : 0u;
@@ -377,7 +455,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       float z = 0.0f;
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
-        if (lane + 64 * i < E) z += __expf(lv[i] - m);
+        if (4 * lane + i < E) z += __expf(lv[i] - m);
       z = wave_sum(z);
       // slot j is handled by lane j
       uint32_t my = 0;
@@ -410,7 +488,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     // ---- routed loads: parameters first, then packed words.
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-      const int q = gwave + pp * n_waves;
+      const int q = pw + pp * n_waves;
       const int u = q / I;
       if (q < n_pairs && u < K)
         load_pair_params<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
@@ -420,7 +498,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     issue_fence();
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-      const int q = gwave + pp * n_waves;
+      const int q = pw + pp * n_waves;
       const int u = q / I;
       if (q < n_pairs && u < K)
         load_pair_words<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
@@ -451,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     }
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-      const int q = gwave + pp * n_waves;
+      const int q = pw + pp * n_waves;
       if (q >= n_pairs) continue;  // wave-uniform
       float au = 0.0f, ag = 0.0f;
 #pragma unroll
@@ -475,15 +553,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- the next layer's routing-independent loads overlap this layer's
-    // hand-over and down projection.
-    if (!last) {
-      const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
-      const int n_rows_n = E + ((p.has_shared && Ln.sgate_w) ? 1 : 0);
-      issue_prologue<BITS, CPL, NP, RC>(Ln, row, n_rows_n, E, p.has_shared, K, gwave, n_waves,
-                                        n_pairs, h, lane, rw, pr, dr_next, dpw1_next);
-    }
-
     // ---- down scales / biases of every unit, ready before act arrives.
     const int gd = lane >> 3;
     float dsc[NU], dbi[NU];
@@ -493,25 +562,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       dbi[uu] = uu == NU - 1 ? param_of(dpw1, 4, gd) : param_of(dpw0, uu * 8 + 4, gd);
     }
 
-    // ---- poll every act word (9 per thread) into LDS.
-    {
-      uint32_t v[kStageAct];
-      for (int spin = 0;; ++spin) {
-        bool ok = true;
-#pragma unroll
-        for (int j = 0; j < kStageAct; ++j) {
-          const int i = threadIdx.x + j * kThreads;
-          v[j] = i < n_pairs ? load_coherent_u32(sc->act + i) : 0u;
-          ok &= i >= n_pairs || tag_ok(v[j], tag_act);
-        }
-        if (ok) break;
-        if (spin >= kSpinLimit) { timed_out = true; break; }
-        __builtin_amdgcn_s_sleep(1);
-      }
-#pragma unroll
-      for (int j = 0; j < kStageAct; ++j)
-        s_act[threadIdx.x + j * kThreads] = __uint_as_float(v[j] & 0xFFFF0000u);
-    }
+    // ---- collect every act word into LDS.
+    if (wave >= kWaves - kActPollWaves)
+      poll_tagged<NU * I / 256 / kActPollWaves>(sc->act, n_pairs, tag_act, s_act, lane,
+                                                wave - (kWaves - kActPollWaves), timed_out);
     __syncthreads();
     // sum of act over each lane's 8 values of each unit, shared by all waves
     for (int i = threadIdx.x; i < U * 64; i += kThreads) {
@@ -554,12 +608,13 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         }
         ys[uu] = dsc[uu] * qa + dbi[uu] * asum;
       }
+      wave_sum_n<NU>(ys);
       float acc = 0.0f;
 #pragma unroll
       for (int uu = 0; uu < NU; ++uu) {
         const int u = uu == NU - 1 ? K : uu;
         const bool on = uu == NU - 1 ? (p.has_shared != 0) : (uu < K);
-        if (on) acc += s_coef[u] * round_bf16(wave_sum(ys[uu]));
+        if (on) acc += s_coef[u] * round_bf16(ys[uu]);
       }
       if (lane == 0) {
         float o = round_bf16(acc);
@@ -574,8 +629,18 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
           store_coherent_u32(sc->xs[layer & 1] + h, tagged(ob, tag_x));
       }
     }
-    dr[NU - 1] = dr_next;
-    dpw1 = dpw1_next;
+    // The next layer's routing-independent loads go out now that this
+    // layer's down rows are done: issued earlier they would sit in front of
+    // the hand-over polls of their wave (a wave's loads return in order).
+    // The polls use waves that carry the fewest of them (x: waves 4-7, act:
+    // 2-7, logits: 7; router rows and shared pairs sit on waves 0 and 1).
+    if (!last) {
+      const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
+      const int n_rows_n = E + ((p.has_shared && Ln.sgate_w) ? 1 : 0);
+      issue_router_and_shared_down<BITS, RC>(Ln, row, n_rows_n, E, p.has_shared, h, lane, rw,
+                                             dr[NU - 1], dpw1);
+      issue_shared_pairs<BITS, CPL, NP>(Ln, p.has_shared, K, pw, n_waves, n_pairs, lane, pr);
+    }
     // s_x / s_act / s_idx are rewritten by the next layer
     __syncthreads();
   }
