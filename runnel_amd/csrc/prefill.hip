@@ -52,11 +52,18 @@ constexpr int kGemmThreads = 256;               // 4 waves
 constexpr int kDownTileN = 2 * kPrefillTileN;   // down columns per workgroup
 constexpr int kPad = 8;                         // bf16 of padding per LDS row
 
-template <int BITS, int BM>
+// K advances in chunks of KC values.  Each lane group g = l / 16 owns KC / 4
+// consecutive values of a weight row per chunk, so a chunk reads 128
+// contiguous bytes of every row (a whole cache line): 8-bit rows in chunks
+// of 128 values, 4-bit rows in chunks of 256 where the A tile still fits
+// (32-row tiles over K = H, a multiple of 256), else 128.
+template <int BITS, int BM, int MODE>
 struct Chunk {
-  static constexpr int KC = BITS == 8 ? 64 : 128;      // k values per chunk
+  static constexpr int KC = BITS == 8 ? 128 : ((BM == 32 && MODE == 0) ? 256 : 128);
   static constexpr int NJ = KC / 32;                   // MFMAs per chunk
   static constexpr int WORDS = KC * BITS / 32;         // u32 per row per chunk
+  static constexpr int LANE_WORDS = WORDS / 4;         // u32 per lane per row
+  static constexpr int LPC = LANE_WORDS / 4;           // 16-byte loads per lane per row
   static constexpr int ROW = KC + kPad;                // LDS row (bf16)
   static constexpr int PIECES = BM * KC / 8;           // 16-byte A pieces
   static constexpr int PPT = PIECES / kGemmThreads;    // pieces per thread
@@ -68,20 +75,25 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
-// The bf16 MFMA fragment j (8 consecutive k) of a lane's 16-byte weight load.
-template <int BITS>
-__device__ __forceinline__ bf16x8_t dequant_frag(const uint4 w, int j, float s, float b) {
-  u32x4 d;
+__device__ __forceinline__ uint32_t word_of(const uint4 v, int c) {
+  return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+}
 
+// The bf16 MFMA fragment j (8 consecutive k) of a lane's weight slice (LPC
+// 16-byte loads).
+template <int BITS, int LPC>
+__device__ __forceinline__ bf16x8_t dequant_frag(const uint4 (&w)[LPC], int j, float s,
+                                                 float b) {
+  u32x4 d;
   if constexpr (BITS == 8) {
-    const uint32_t w0 = j == 0 ? w.x : w.z;
-    const uint32_t w1 = j == 0 ? w.y : w.w;
+    const uint32_t w0 = word_of(w[j >> 1], 2 * (j & 1));
+    const uint32_t w1 = word_of(w[j >> 1], 2 * (j & 1) + 1);
     d.x = pack_bf16x2(fmaf((float)(w0 & 0xFFu), s, b), fmaf((float)((w0 >> 8) & 0xFFu), s, b));
     d.y = pack_bf16x2(fmaf((float)((w0 >> 16) & 0xFFu), s, b), fmaf((float)(w0 >> 24), s, b));
     d.z = pack_bf16x2(fmaf((float)(w1 & 0xFFu), s, b), fmaf((float)((w1 >> 8) & 0xFFu), s, b));
     d.w = pack_bf16x2(fmaf((float)((w1 >> 16) & 0xFFu), s, b), fmaf((float)(w1 >> 24), s, b));
   } else {
-    const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+    const uint32_t wj = word_of(w[j >> 2], j & 3);
     const uint32_t lo = wj & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
     const uint32_t hi = (wj >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
     d.x = pack_bf16x2(fmaf((float)(lo & 0xFFu), s, b), fmaf((float)(hi & 0xFFu), s, b));
@@ -239,7 +251,7 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
 // rows are multiplied (two specialisations: all blocks, or the first half).
 template <int BITS, int BM, int MODE>
 struct Gemm {
-  using C = Chunk<BITS, BM>;
+  using C = Chunk<BITS, BM, MODE>;
   static constexpr int MB = BM / 16;
   static constexpr int TN = MODE == 0 ? kPrefillTileN : kDownTileN;
 
@@ -275,7 +287,7 @@ struct Gemm {
         const int c = tile.n * TN + wave * 64 + qq * 16 + col_l;
         brow[qq] = e * p.H + (size_t)c;
       }
-      wptr[qq] = q.w + brow[qq] * WPR + kg * 4;
+      wptr[qq] = q.w + brow[qq] * WPR + kg * C::LANE_WORDS;
     }
   }
 
@@ -316,17 +328,19 @@ struct Gemm {
   }
   // Scales and biases stay raw bf16 bits until the chunk that uses them, so
   // a prefetch is never waited for where it is issued.
-  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[4], uint32_t (&s)[4],
+  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[4][C::LPC], uint32_t (&s)[4],
                                          uint32_t (&b)[4]) const {
     const int G = K / 64;
-    const int g = BITS == 8 ? ch : 2 * ch + (kg >> 1);
+    const int g = (ch * C::KC + kg * (C::KC / 4)) >> 6;  // this lane's group
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       s[qq] = q.s[brow[qq] * G + g];
       b[qq] = q.b[brow[qq] * G + g];
     }
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) w[qq] = load16_stream(wptr[qq] + ch * C::WORDS);
+    for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+      for (int l = 0; l < C::LPC; ++l) w[qq][l] = load16_stream(wptr[qq] + ch * C::WORDS + 4 * l);
   }
 
   // One chunk of KC: NJ MFMA steps over the first MBA row blocks.  The LDS
@@ -334,7 +348,7 @@ struct Gemm {
   // MFMAs of step j, so the matrix core, the vector ALU and the LDS of the
   // SIMD work at the same time.
   template <int MBA>
-  __device__ __forceinline__ void chunk(int buf, const uint4 (&w)[4], const uint32_t (&sraw)[4],
+  __device__ __forceinline__ void chunk(int buf, const uint4 (&w)[4][C::LPC], const uint32_t (&sraw)[4],
                                         const uint32_t (&braw)[4], f32x4_t (&acc)[MB][4]) const {
     const uint16_t* sa = &s_a[buf][col_l * C::ROW + kg * (C::KC / 4)];
     float s[4], b[4];
@@ -352,14 +366,15 @@ struct Gemm {
     bf16x8_t a[MBA], bf[4];
     read_a(0, a);
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) bf[qq] = dequant_frag<BITS>(w[qq], 0, s[qq], b[qq]);
+    for (int qq = 0; qq < 4; ++qq) bf[qq] = dequant_frag<BITS, C::LPC>(w[qq], 0, s[qq], b[qq]);
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
       bf16x8_t na[MBA], nbf[4];
       if (j + 1 < C::NJ) {
         read_a(j + 1, na);
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) nbf[qq] = dequant_frag<BITS>(w[qq], j + 1, s[qq], b[qq]);
+        for (int qq = 0; qq < 4; ++qq)
+          nbf[qq] = dequant_frag<BITS, C::LPC>(w[qq], j + 1, s[qq], b[qq]);
       }
 #pragma unroll
       for (int mb = 0; mb < MBA; ++mb)
@@ -389,7 +404,7 @@ struct Gemm {
     const uint16_t* asrc[C::PPT];
     a_rows(asrc);
     uint4 ar[C::PPT];
-    uint4 bw[4];
+    uint4 bw[4][C::LPC];
     uint32_t bs[4], bb[4];
     load_b(0, bw, bs, bb);
     load_a(0, asrc, ar);
@@ -400,7 +415,7 @@ struct Gemm {
       // the prefetch is unconditional (the last chunk loads itself again)
       // so no branch splits the loop body
       const int nx = min(ch + 1, nch - 1);
-      uint4 nw[4];
+      uint4 nw[4][C::LPC];
       uint32_t ns[4], nb[4];
       load_b(nx, nw, ns, nb);
       load_a(nx, asrc, ar);
@@ -409,7 +424,8 @@ struct Gemm {
       __syncthreads();
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        bw[qq] = nw[qq];
+#pragma unroll
+        for (int l = 0; l < C::LPC; ++l) bw[qq][l] = nw[qq][l];
         bs[qq] = ns[qq];
         bb[qq] = nb[qq];
       }

@@ -179,3 +179,36 @@ def test_graph_replays_equal_eager_calls(torch_cuda, bits):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {r}"
     assert native.workspace_status(ws) == 0
+
+
+def test_thousand_step_4bit_decode(torch_cuda):
+    """The 4-bit decode workload: 1000 seeded batch-1 steps through one
+    full-size 4-bit layer (one single-launch call per step).  Routing is
+    bit-exact with the oracle on every step; outputs are held to the
+    contract and north-star tolerances on 64 sampled steps."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lw = synthetic.make_layer(0, bits=4)
+    h = lw.handle()
+    xs = synthetic.make_x(1000, 1000, 2048)
+    ws = torch.zeros(h.workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    outs = torch.empty_like(xs)
+    idx = torch.empty((1000, 8), dtype=torch.int32, device="cuda")
+    for t in range(1000):
+        o, i, _ = native.moe_block(h, xs[t:t + 1], return_routing=True, workspace=ws)
+        outs[t:t + 1].copy_(o)
+        idx[t:t + 1].copy_(i)
+    torch.cuda.synchronize()
+    assert native.workspace_status(ws) == 0
+    L = layer_from_dev(lw)
+    xb = host_bf16(xs)
+    ref_idx, _, _ = M.route(xb, L.router_w, 8)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    few = np.random.default_rng(1).choice(1000, 64, replace=False)
+    ref, _, _ = M.block_forward(L, xb[few])
+    got = host_bf16(outs)[few]
+    assert _contract_mismatches(got, ref) <= got.size // 500
+    mlx, _, _ = M.block_forward(L, xb[few], mode="mlx")
+    g = M.bf16_to_f32(got)
+    assert np.abs(g - M.bf16_to_f32(mlx)).max() <= MAX_ABS
+    assert cosine(g, M.bf16_to_f32(mlx)) >= MIN_COS
