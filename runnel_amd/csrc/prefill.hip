@@ -48,7 +48,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
-constexpr int kGemmThreads = 256;               // 4 waves
 constexpr int kDownTileN = 2 * kPrefillTileN;   // down columns per workgroup
 constexpr int kPad = 8;                         // bf16 of padding per LDS row
 
@@ -59,6 +58,13 @@ constexpr int kPad = 8;                         // bf16 of padding per LDS row
 // (32-row tiles over K = H, a multiple of 256), else 128.
 template <int BITS, int BM, int MODE>
 struct Chunk {
+  // 32-row tiles (short prefill, memory bound) run 8 waves of 2 column
+  // blocks each: half the registers per wave, twice the loads in flight per
+  // CU.  128-row tiles run 4 waves of 4 blocks (each A fragment read from
+  // LDS feeds 4 MFMAs).
+  static constexpr int THREADS = 512;
+  static constexpr int QPW = 2;                        // 16-column blocks per wave
+  static constexpr int MIN_WAVES = BM == 32 ? 4 : 2;   // waves per SIMD
   static constexpr int KC = BITS == 8 ? 128 : ((BM == 32 && MODE == 0) ? 256 : 128);
   static constexpr int NJ = KC / 32;                   // MFMAs per chunk
   static constexpr int WORDS = KC * BITS / 32;         // u32 per row per chunk
@@ -66,8 +72,8 @@ struct Chunk {
   static constexpr int LPC = LANE_WORDS / 4;           // 16-byte loads per lane per row
   static constexpr int ROW = KC + kPad;                // LDS row (bf16)
   static constexpr int PIECES = BM * KC / 8;           // 16-byte A pieces
-  static constexpr int PPT = PIECES / kGemmThreads;    // pieces per thread
-  static_assert(PIECES % kGemmThreads == 0, "A tile must split evenly");
+  static constexpr int PPT = PIECES / THREADS;         // pieces per thread
+  static_assert(PIECES % THREADS == 0, "A tile must split evenly");
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -261,8 +267,10 @@ struct Gemm {
   const int* s_row;
   int tid, wave, lane, col_l, kg, K;
   QW q;
-  size_t brow[4];
-  const uint32_t* wptr[4];
+  static constexpr int QPW = C::QPW;
+  static constexpr int THREADS = C::THREADS;
+  size_t brow[QPW];
+  const uint32_t* wptr[QPW];
 
   __device__ Gemm(const PrefillArgs& p_, const Tile& t_, uint16_t (*sa)[BM * C::ROW],
                   const int* srow)
@@ -277,14 +285,15 @@ struct Gemm {
     K = MODE == 0 ? p.H : p.I;
     const int WPR = K * BITS / 32;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
+    for (int qq = 0; qq < QPW; ++qq) {
       if constexpr (MODE == 0) {
+        // blocks 0 .. QPW/2-1: up rows of this wave's pairs, then gate rows
         q = shared ? p.sgu : p.gu;
-        const int c = tile.n * TN + wave * 32 + (qq & 1) * 16 + col_l;
-        brow[qq] = e * 2 * p.I + (size_t)(c + (qq >> 1) * p.I);
+        const int c = tile.n * TN + wave * (8 * QPW) + (qq % (QPW / 2)) * 16 + col_l;
+        brow[qq] = e * 2 * p.I + (size_t)(c + (qq / (QPW / 2)) * p.I);
       } else {
         q = shared ? p.sdn : p.dn;
-        const int c = tile.n * TN + wave * 64 + qq * 16 + col_l;
+        const int c = tile.n * TN + wave * (16 * QPW) + qq * 16 + col_l;
         brow[qq] = e * p.H + (size_t)c;
       }
       wptr[qq] = q.w + brow[qq] * WPR + kg * C::LANE_WORDS;
@@ -296,7 +305,7 @@ struct Gemm {
   __device__ __forceinline__ void a_rows(const uint16_t* (&src)[C::PPT]) const {
 #pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
-      const int pi = tid + kGemmThreads * j;
+      const int pi = tid + THREADS * j;
       const int r = pi / (C::KC / 8);
       const int c8 = pi - r * (C::KC / 8);
       src[j] = nullptr;
@@ -320,7 +329,7 @@ struct Gemm {
   __device__ __forceinline__ void store_a(int buf, const uint4 (&ar)[C::PPT]) const {
 #pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
-      const int pi = tid + kGemmThreads * j;
+      const int pi = tid + THREADS * j;
       const int r = pi / (C::KC / 8);
       const int c8 = pi - r * (C::KC / 8);
       *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) = ar[j];
@@ -328,17 +337,17 @@ struct Gemm {
   }
   // Scales and biases stay raw bf16 bits until the chunk that uses them, so
   // a prefetch is never waited for where it is issued.
-  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[4][C::LPC], uint32_t (&s)[4],
-                                         uint32_t (&b)[4]) const {
+  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[QPW][C::LPC], uint32_t (&s)[QPW],
+                                         uint32_t (&b)[QPW]) const {
     const int G = K / 64;
     const int g = (ch * C::KC + kg * (C::KC / 4)) >> 6;  // this lane's group
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
+    for (int qq = 0; qq < QPW; ++qq) {
       s[qq] = q.s[brow[qq] * G + g];
       b[qq] = q.b[brow[qq] * G + g];
     }
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq)
+    for (int qq = 0; qq < QPW; ++qq)
 #pragma unroll
       for (int l = 0; l < C::LPC; ++l) w[qq][l] = load16_stream(wptr[qq] + ch * C::WORDS + 4 * l);
   }
@@ -348,12 +357,13 @@ struct Gemm {
   // MFMAs of step j, so the matrix core, the vector ALU and the LDS of the
   // SIMD work at the same time.
   template <int MBA>
-  __device__ __forceinline__ void chunk(int buf, const uint4 (&w)[4][C::LPC], const uint32_t (&sraw)[4],
-                                        const uint32_t (&braw)[4], f32x4_t (&acc)[MB][4]) const {
+  __device__ __forceinline__ void chunk(int buf, const uint4 (&w)[QPW][C::LPC],
+                                        const uint32_t (&sraw)[QPW], const uint32_t (&braw)[QPW],
+                                        f32x4_t (&acc)[MB][QPW]) const {
     const uint16_t* sa = &s_a[buf][col_l * C::ROW + kg * (C::KC / 4)];
-    float s[4], b[4];
+    float s[QPW], b[QPW];
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
+    for (int qq = 0; qq < QPW; ++qq) {
       s[qq] = bf16_to_f32(sraw[qq]);
       b[qq] = bf16_to_f32(braw[qq]);
     }
@@ -363,49 +373,49 @@ struct Gemm {
         a[mb] = __builtin_bit_cast(
             bf16x8_t, *reinterpret_cast<const u32x4*>(sa + mb * 16 * C::ROW + 8 * j));
     };
-    bf16x8_t a[MBA], bf[4];
+    bf16x8_t a[MBA], bf[QPW];
     read_a(0, a);
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) bf[qq] = dequant_frag<BITS, C::LPC>(w[qq], 0, s[qq], b[qq]);
+    for (int qq = 0; qq < QPW; ++qq) bf[qq] = dequant_frag<BITS, C::LPC>(w[qq], 0, s[qq], b[qq]);
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
-      bf16x8_t na[MBA], nbf[4];
+      bf16x8_t na[MBA], nbf[QPW];
       if (j + 1 < C::NJ) {
         read_a(j + 1, na);
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq)
+        for (int qq = 0; qq < QPW; ++qq)
           nbf[qq] = dequant_frag<BITS, C::LPC>(w[qq], j + 1, s[qq], b[qq]);
       }
 #pragma unroll
       for (int mb = 0; mb < MBA; ++mb)
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) acc[mb][qq] = mfma(a[mb], bf[qq], acc[mb][qq]);
+        for (int qq = 0; qq < QPW; ++qq) acc[mb][qq] = mfma(a[mb], bf[qq], acc[mb][qq]);
       if (j + 1 < C::NJ) {
         // per MFMA: one MFMA, a share of the next step's LDS reads and of
         // its dequantisation
-        constexpr int kValuPer = (BITS == 8 ? 80 : 112) / (4 * MBA) + 1;
+        constexpr int kValuPer = (BITS == 8 ? 20 : 28) / MBA + 1;
 #pragma unroll
-        for (int i = 0; i < 4 * MBA; ++i) {
+        for (int i = 0; i < QPW * MBA; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (i % 4 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (i % QPW == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
         }
 #pragma unroll
         for (int mb = 0; mb < MBA; ++mb) a[mb] = na[mb];
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) bf[qq] = nbf[qq];
+        for (int qq = 0; qq < QPW; ++qq) bf[qq] = nbf[qq];
       }
     }
   }
 
   template <int MBA>
-  __device__ void run(f32x4_t (&acc)[MB][4]) const {
+  __device__ void run(f32x4_t (&acc)[MB][QPW]) const {
     const int nch = K / C::KC;
     const uint16_t* asrc[C::PPT];
     a_rows(asrc);
     uint4 ar[C::PPT];
-    uint4 bw[4][C::LPC];
-    uint32_t bs[4], bb[4];
+    uint4 bw[QPW][C::LPC];
+    uint32_t bs[QPW], bb[QPW];
     load_b(0, bw, bs, bb);
     load_a(0, asrc, ar);
     store_a(0, ar);
@@ -415,15 +425,15 @@ struct Gemm {
       // the prefetch is unconditional (the last chunk loads itself again)
       // so no branch splits the loop body
       const int nx = min(ch + 1, nch - 1);
-      uint4 nw[4][C::LPC];
-      uint32_t ns[4], nb[4];
+      uint4 nw[QPW][C::LPC];
+      uint32_t ns[QPW], nb[QPW];
       load_b(nx, nw, ns, nb);
       load_a(nx, asrc, ar);
       chunk<MBA>(buf, bw, bs, bb, acc);
       store_a(buf ^ 1, ar);
       __syncthreads();
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
+      for (int qq = 0; qq < QPW; ++qq) {
 #pragma unroll
         for (int l = 0; l < C::LPC; ++l) bw[qq][l] = nw[qq][l];
         bs[qq] = ns[qq];
@@ -432,7 +442,7 @@ struct Gemm {
     }
   }
 
-  __device__ void epilogue(const f32x4_t (&acc)[MB][4], int mba) const {
+  __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       if (mb >= mba) continue;
@@ -442,16 +452,16 @@ struct Gemm {
         if (r >= tile.nrows) continue;
         if constexpr (MODE == 0) {
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int c = tile.n * TN + wave * 32 + h * 16 + col_l;
+          for (int h = 0; h < QPW / 2; ++h) {
+            const int c = tile.n * TN + wave * (8 * QPW) + h * 16 + col_l;
             const float up = round_bf16(acc[mb][h][i]);
-            const float gate = round_bf16(acc[mb][2 + h][i]);
+            const float gate = round_bf16(acc[mb][QPW / 2 + h][i]);
             p.act[(size_t)(tile.row0 + r) * p.I + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
           }
         } else {
 #pragma unroll
-          for (int qq = 0; qq < 4; ++qq) {
-            const int c = tile.n * TN + wave * 64 + qq * 16 + col_l;
+          for (int qq = 0; qq < QPW; ++qq) {
+            const int c = tile.n * TN + wave * (16 * QPW) + qq * 16 + col_l;
             p.y[(size_t)s_row[r] * p.H + c] = (uint16_t)f32_to_bf16(acc[mb][qq][i]);
           }
         }
@@ -461,7 +471,9 @@ struct Gemm {
 };
 
 template <int BITS, int BM, int MODE>
-__global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(const PrefillArgs p,
+__global__ __launch_bounds__((Chunk<BITS, BM, MODE>::THREADS))
+__attribute__((amdgpu_waves_per_eu(Chunk<BITS, BM, MODE>::MIN_WAVES))) void prefill_gemm_kernel(
+    const PrefillArgs p,
                                                                      const int nt) {
   using G = Gemm<BITS, BM, MODE>;
   __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * G::C::ROW];
@@ -482,7 +494,7 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(const Prefil
   __syncthreads();
   if (tile.bucket == p.E + 1) {
     // out-of-range expert ids: zero rows, nothing loaded
-    for (int i = tid; i < tile.nrows * G::TN; i += kGemmThreads) {
+    for (int i = tid; i < tile.nrows * G::TN; i += G::THREADS) {
       const int r = i / G::TN;
       const int c = tile.n * G::TN + (i - r * G::TN);
       if constexpr (MODE == 0)
@@ -493,11 +505,11 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(const Prefil
     return;
   }
   const G g(p, tile, s_a, s_row);
-  f32x4_t acc[G::MB][4];
+  f32x4_t acc[G::MB][G::QPW];
 #pragma unroll
   for (int mb = 0; mb < G::MB; ++mb)
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) acc[mb][qq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int qq = 0; qq < G::QPW; ++qq) acc[mb][qq] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int mba = (tile.nrows + 15) >> 4;
   if (mba > G::MB / 2) {
     g.template run<G::MB>(acc);
@@ -581,9 +593,11 @@ void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
   const int nt_dn = a.H / kDownTileN;
   const int g_gu = 8 * ((nt_gu * mt + 7) / 8);
   const int g_dn = 8 * ((nt_dn * mt + 7) / 8);
-  hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu), dim3(kGemmThreads), 0, s,
+  hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu),
+                     dim3(Chunk<BITS, BM, 0>::THREADS), 0, s,
                      a, nt_gu);
-  hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn), dim3(kGemmThreads), 0, s,
+  hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn),
+                     dim3(Chunk<BITS, BM, 1>::THREADS), 0, s,
                      a, nt_dn);
 }
 
