@@ -127,6 +127,7 @@ struct PrefillArgs {
   int32_t* rows;           // [T K + T] source row of each sorted row
   int32_t* offs;           // [E + 3] rows per bucket (E: shared, E + 1: bad ids)
   int32_t* tile_offs;      // [E + 3] m-tiles per bucket; [E + 2] = total
+  int32_t* tile_desc;      // [m-tiles][4]: bucket, first sorted row, rows, 0
   uint16_t* act;           // [T K + T, I] bf16, sorted order
   uint16_t* y;             // [T K (+ T), H] bf16 at row t K + j (shared: T K + t)
   const float* scores;     // [T, K + 1] router scores, slot K = shared gate

@@ -122,10 +122,12 @@ struct Tile {
   int n, bucket, row0, nrows;
 };
 
-template <int BM>
+// Items are (m-tile, n-tile) with n innermost, cut into 8 contiguous runs,
+// one per XCD (workgroup i runs on XCD i % 8): the n-tiles of one m-tile
+// share its A rows in that XCD's L2, and the m-tiles of one expert share
+// its weight columns there.
 __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& t) {
-  const int NB = p.E + 2;
-  const int MT = p.tile_offs[NB];
+  const int MT = p.tile_offs[p.E + 2];
   const int total = nt * MT;
   const int L = (total + 7) >> 3;
   const int xcd = blockIdx.x & 7;
@@ -133,17 +135,12 @@ __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& 
   if (slot >= L) return false;
   const int item = xcd * L + slot;
   if (item >= total) return false;
-  t.n = item / MT;
-  const int rem = item - t.n * MT;
-  int lo = 0, hi = NB - 1;  // last bucket whose first tile is <= rem
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.tile_offs[mid] <= rem) lo = mid;
-    else hi = mid - 1;
-  }
-  t.bucket = lo;
-  t.row0 = p.offs[lo] + (rem - p.tile_offs[lo]) * BM;
-  t.nrows = min(BM, p.offs[lo + 1] - t.row0);
+  const int m = item / nt;
+  t.n = item - m * nt;
+  const int4 d = reinterpret_cast<const int4*>(p.tile_desc)[m];
+  t.bucket = d.x;
+  t.row0 = d.y;
+  t.nrows = d.z;
   return true;
 }
 
@@ -201,6 +198,13 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
     if (tid == NB - 1) {
       p.offs[NB] = s_scan[0][tid];
       p.tile_offs[NB] = s_scan[1][tid];
+    }
+    // this bucket's m-tiles
+    const int t0 = s_scan[1][tid] - tiles_b;
+    for (int i = 0; i < tiles_b; ++i) {
+      const int r = row_off + i * p.bm;
+      *reinterpret_cast<int4*>(p.tile_desc + 4 * (t0 + i)) =
+          make_int4(tid, r, min(p.bm, row_off + rows_b - r), 0);
     }
     // per-wave bases of this bucket (stable: wave order = row order)
     int base = row_off;
@@ -479,7 +483,7 @@ __attribute__((amdgpu_waves_per_eu(Chunk<BITS, BM, MODE>::MIN_WAVES))) void pref
   __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * G::C::ROW];
   __shared__ int s_row[BM];
   Tile tile;
-  if (!decode_tile<BM>(p, nt, tile)) return;
+  if (!decode_tile(p, nt, tile)) return;
   const int tid = threadIdx.x;
   const int TK = p.T * p.K;
   if (tid < BM) {
