@@ -7,26 +7,27 @@
 //                           (token, slot) rows by expert id (mlx-lm
 //                           _gather_sort order), the shared expert's rows
 //                           appended as bucket E, out-of-range ids as
-//                           bucket E + 1; row and m-tile offsets per bucket.
-//   prefill_gate_up_kernel  one (bucket, m-tile of 128 rows, n-tile of 128
-//                           [up; gate] pairs) per workgroup: the x rows of
-//                           the tile staged in LDS, every wave streams its
-//                           own 32 up and 32 gate weight rows straight from
-//                           HBM into registers, dequantises them to bf16
-//                           (fl32(q*s + b) rounded to nearest even) and
-//                           feeds v_mfma_f32_16x16x32_bf16; SwiGLU epilogue,
-//                           bf16 activations in sorted row order.
-//   prefill_down_kernel     the same over the activations (already in
-//                           sorted order, contiguous) and the down bank, 256
-//                           output columns per workgroup; bf16 rows written
-//                           to their (token, slot) place.
+//                           bucket E + 1; row and m-tile offsets per bucket
+//                           and one descriptor per m-tile.
+//   prefill_gemm_kernel     MODE 0 (gate/up): one (m-tile, n-tile of [up;
+//                           gate] pairs) per workgroup; the x rows of the
+//                           tile staged in LDS, every wave streams its own
+//                           up and gate weight rows straight from HBM into
+//                           registers, dequantises them to bf16 (fl32(q*s +
+//                           b) rounded to nearest even) and feeds
+//                           v_mfma_f32_16x16x32_bf16; SwiGLU epilogue, bf16
+//                           activations in sorted row order.
+//                           MODE 1 (down): the same over the activations
+//                           (contiguous in sorted order) and the down bank;
+//                           bf16 rows written to their (token, slot) place.
 //   prefill_combine_kernel  per token: sum of score * row over the slots and
 //                           the gated shared row, residual, bf16.
 //
-// Work items are ordered (n-tile, bucket, m-tile) and cut into eight equal
-// contiguous runs, one per XCD (workgroup i runs on XCD i % 8): the m-tiles
-// of one (bucket, n-tile) run back to back on one XCD, so their common
-// weight tile is read from HBM once and then hit in that XCD's L2.
+// Tiles are 32 rows (short prefill: memory bound, few rows per expert) or
+// 128 rows (long prefill: matrix-core bound).  A workgroup is 8 waves (two
+// per SIMD: a single wave per SIMD issues vector instructions too slowly to
+// keep the dequantisation beside the MFMAs); each wave owns 32 weight
+// columns of the tile.
 //
 // MFMA operand layout (16x16x32 bf16, checked on the device): lane l holds
 // A row l % 16 and B column l % 16, k = 8 (l / 16) + [0, 8); D column l % 16,
@@ -48,7 +49,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
-constexpr int kDownTileN = 2 * kPrefillTileN;   // down columns per workgroup
 constexpr int kPad = 8;                         // bf16 of padding per LDS row
 
 // K advances in chunks of KC values.  Each lane group g = l / 16 owns KC / 4
@@ -58,13 +58,9 @@ constexpr int kPad = 8;                         // bf16 of padding per LDS row
 // (32-row tiles over K = H, a multiple of 256), else 128.
 template <int BITS, int BM, int MODE>
 struct Chunk {
-  // 32-row tiles (short prefill, memory bound) run 8 waves of 2 column
-  // blocks each: half the registers per wave, twice the loads in flight per
-  // CU.  128-row tiles run 4 waves of 4 blocks (each A fragment read from
-  // LDS feeds 4 MFMAs).
-  static constexpr int THREADS = 512;
+  static constexpr int THREADS = 512;                  // 8 waves
   static constexpr int QPW = 2;                        // 16-column blocks per wave
-  static constexpr int MIN_WAVES = BM == 32 ? 4 : 2;   // waves per SIMD
+  static constexpr int MIN_WAVES = BM == 32 ? 4 : 2;   // waves per SIMD (registers)
   static constexpr int KC = BITS == 8 ? 128 : ((BM == 32 && MODE == 0) ? 256 : 128);
   static constexpr int NJ = KC / 32;                   // MFMAs per chunk
   static constexpr int WORDS = KC * BITS / 32;         // u32 per row per chunk
@@ -116,7 +112,7 @@ __device__ __forceinline__ f32x4_t mfma(const bf16x8_t a, const bf16x8_t b, cons
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Work item of this workgroup: (n-tile, bucket, m-tile).  Returns false when
+// Work item of this workgroup: (n-tile, bucket, rows).  Returns false when
 // the workgroup has nothing to do.
 struct Tile {
   int n, bucket, row0, nrows;
@@ -263,7 +259,8 @@ template <int BITS, int BM, int MODE>
 struct Gemm {
   using C = Chunk<BITS, BM, MODE>;
   static constexpr int MB = BM / 16;
-  static constexpr int TN = MODE == 0 ? kPrefillTileN : kDownTileN;
+  // columns per workgroup: gate/up pairs (two rows each) or down columns
+  static constexpr int TN = (C::THREADS / 64) * 16 * C::QPW / (MODE == 0 ? 2 : 1);
 
   const PrefillArgs& p;
   const Tile& tile;
@@ -304,39 +301,49 @@ struct Gemm {
     }
   }
 
-  // This thread's A pieces: row base pointers, fixed for the whole tile
-  // (null for rows past the tile's end).
-  __device__ __forceinline__ void a_rows(const uint16_t* (&src)[C::PPT]) const {
+  // This thread's A pieces: row base pointers, fixed for the whole tile.
+  // Rows past the tile's end read a row that exists (x row of token 0, or
+  // the tile's last row) and are stored as zeros, so every load is
+  // unconditional and the compiler can count the loads still in flight.
+  __device__ __forceinline__ void a_rows(const uint16_t* (&src)[C::PPT],
+                                         bool (&live)[C::PPT]) const {
 #pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
       const int pi = tid + THREADS * j;
       const int r = pi / (C::KC / 8);
       const int c8 = pi - r * (C::KC / 8);
-      src[j] = nullptr;
-      if (r < tile.nrows) {
-        if constexpr (MODE == 0)
-          src[j] = p.x + (size_t)s_row[r] * p.H + c8 * 8;
-        else
-          src[j] = p.act + (size_t)(tile.row0 + r) * p.I + c8 * 8;
-      }
+      live[j] = r < tile.nrows;
+      if constexpr (MODE == 0)
+        src[j] = p.x + (size_t)s_row[r] * p.H + c8 * 8;  // s_row is 0 past the end
+      else
+        src[j] = p.act + (size_t)(tile.row0 + min(r, tile.nrows - 1)) * p.I + c8 * 8;
     }
   }
 
   __device__ __forceinline__ void load_a(int ch, const uint16_t* const (&src)[C::PPT],
                                          uint4 (&ar)[C::PPT]) const {
 #pragma unroll
+    for (int j = 0; j < C::PPT; ++j) ar[j] = load16(src[j] + ch * C::KC);
+  }
+  // Only the live rows (a memory-bound short tile does not fetch its padding).
+  __device__ __forceinline__ void load_a_live(int ch, const uint16_t* const (&src)[C::PPT],
+                                              const bool (&live)[C::PPT],
+                                              uint4 (&ar)[C::PPT]) const {
+#pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
       ar[j] = make_uint4(0, 0, 0, 0);
-      if (src[j]) ar[j] = load16(src[j] + ch * C::KC);
+      if (live[j]) ar[j] = load16(src[j] + ch * C::KC);
     }
   }
-  __device__ __forceinline__ void store_a(int buf, const uint4 (&ar)[C::PPT]) const {
+  __device__ __forceinline__ void store_a(int buf, const uint4 (&ar)[C::PPT],
+                                          const bool (&live)[C::PPT]) const {
 #pragma unroll
     for (int j = 0; j < C::PPT; ++j) {
       const int pi = tid + THREADS * j;
       const int r = pi / (C::KC / 8);
       const int c8 = pi - r * (C::KC / 8);
-      *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) = ar[j];
+      *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) =
+          live[j] ? ar[j] : make_uint4(0, 0, 0, 0);
     }
   }
   // Scales and biases stay raw bf16 bits until the chunk that uses them, so
@@ -412,29 +419,48 @@ struct Gemm {
     }
   }
 
+  // Chunks are prefetched two ahead: weights into two register sets (B of
+  // chunk c + 2 is issued as soon as chunk c has consumed its set), A into
+  // two register sets that feed the LDS double buffer one chunk ahead.  A
+  // of chunk c + 2 is issued before chunk c's MFMAs and B after them, so
+  // the wait for A of chunk c + 1 leaves both in flight.  Prefetches past
+  // the last chunk reload the last chunk, so no branch splits the loop.
+  template <int MBA, int S>
+  __device__ __forceinline__ void step(int c, int nch, const uint16_t* const (&asrc)[C::PPT],
+                                       const bool (&live)[C::PPT], uint4 (&ar)[2][C::PPT],
+                                       uint4 (&bw)[2][QPW][C::LPC], uint32_t (&bs)[2][QPW],
+                                       uint32_t (&bb)[2][QPW], f32x4_t (&acc)[MB][QPW]) const {
+    load_a(min(c + 2, nch - 1), asrc, ar[S ^ 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    chunk<MBA>(c & 1, bw[S], bs[S], bb[S], acc);
+    load_b(min(c + 2, nch - 1), bw[S], bs[S], bb[S]);
+    store_a((c & 1) ^ 1, ar[S], live);
+    __syncthreads();
+  }
+
+  // 32-row tiles (registers for four waves per SIMD): everything one chunk
+  // ahead.
   template <int MBA>
-  __device__ void run(f32x4_t (&acc)[MB][QPW]) const {
+  __device__ void run1(f32x4_t (&acc)[MB][QPW]) const {
     const int nch = K / C::KC;
     const uint16_t* asrc[C::PPT];
-    a_rows(asrc);
+    bool live[C::PPT];
+    a_rows(asrc, live);
     uint4 ar[C::PPT];
     uint4 bw[QPW][C::LPC];
     uint32_t bs[QPW], bb[QPW];
     load_b(0, bw, bs, bb);
-    load_a(0, asrc, ar);
-    store_a(0, ar);
+    load_a_live(0, asrc, live, ar);
+    store_a(0, ar, live);
     __syncthreads();
     for (int ch = 0; ch < nch; ++ch) {
-      const int buf = ch & 1;
-      // the prefetch is unconditional (the last chunk loads itself again)
-      // so no branch splits the loop body
       const int nx = min(ch + 1, nch - 1);
       uint4 nw[QPW][C::LPC];
       uint32_t ns[QPW], nb[QPW];
       load_b(nx, nw, ns, nb);
-      load_a(nx, asrc, ar);
-      chunk<MBA>(buf, bw, bs, bb, acc);
-      store_a(buf ^ 1, ar);
+      load_a_live(nx, asrc, live, ar);
+      chunk<MBA>(ch & 1, bw, bs, bb, acc);
+      store_a((ch & 1) ^ 1, ar, live);
       __syncthreads();
 #pragma unroll
       for (int qq = 0; qq < QPW; ++qq) {
@@ -444,6 +470,33 @@ struct Gemm {
         bb[qq] = nb[qq];
       }
     }
+  }
+
+  template <int MBA>
+  __device__ void run(f32x4_t (&acc)[MB][QPW]) const {
+    if constexpr (BM == 32) {
+      run1<MBA>(acc);
+      return;
+    }
+    const int nch = K / C::KC;
+    const uint16_t* asrc[C::PPT];
+    bool live[C::PPT];
+    a_rows(asrc, live);
+    uint4 a0[C::PPT], ar[2][C::PPT];
+    uint4 bw[2][QPW][C::LPC];
+    uint32_t bs[2][QPW], bb[2][QPW];
+    load_a(0, asrc, a0);
+    load_b(0, bw[0], bs[0], bb[0]);
+    load_a(min(1, nch - 1), asrc, ar[0]);
+    load_b(min(1, nch - 1), bw[1], bs[1], bb[1]);
+    store_a(0, a0, live);
+    __syncthreads();
+    int ch = 0;
+    for (; ch + 1 < nch; ch += 2) {
+      step<MBA, 0>(ch, nch, asrc, live, ar, bw, bs, bb, acc);
+      step<MBA, 1>(ch + 1, nch, asrc, live, ar, bw, bs, bb, acc);
+    }
+    if (ch < nch) step<MBA, 0>(ch, nch, asrc, live, ar, bw, bs, bb, acc);
   }
 
   __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
@@ -593,8 +646,8 @@ int prefill_max_mtiles(int T, int K, int E, int bm) {
 
 template <int BITS, int BM>
 void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
-  const int nt_gu = a.I / kPrefillTileN;
-  const int nt_dn = a.H / kDownTileN;
+  const int nt_gu = a.I / Gemm<BITS, BM, 0>::TN;
+  const int nt_dn = a.H / Gemm<BITS, BM, 1>::TN;
   const int g_gu = 8 * ((nt_gu * mt + 7) / 8);
   const int g_dn = 8 * ((nt_dn * mt + 7) / 8);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu),
