@@ -136,7 +136,7 @@ size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 struct Layout {
   size_t ctr, fused, logits, idx, scores, act, total;
   // expert-sorted (prefill) path
-  size_t rows, offs, tile_offs, tile_desc, act16, y16, wnorm;
+  size_t rows, offs, tile_offs, tile_desc, hist, act16, y16, wnorm;
 };
 
 // Calls that route at least kPrefillMinRows (token, slot) rows take the
@@ -178,6 +178,8 @@ Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
     off = align_up(off + (size_t)(E + 3) * sizeof(int32_t));
     l.tile_desc = off;  // sized for the smaller tile height (more tiles)
     off = align_up(off + (size_t)rmoe::prefill_max_mtiles(T, K, E, 32) * 4 * sizeof(int32_t));
+    l.hist = off;
+    off = align_up(off + (size_t)rmoe::prefill_sort_slices(T, K) * (E + 2) * sizeof(int32_t));
     l.wnorm = off;
     off = align_up(off + (size_t)E * sizeof(float));
     l.act16 = off;
@@ -211,6 +213,7 @@ rmoe::PrefillArgs prefill_args(const Layout& l, void* ws, int T, int H, int I, i
   a.offs = reinterpret_cast<int32_t*>(base + l.offs);
   a.tile_offs = reinterpret_cast<int32_t*>(base + l.tile_offs);
   a.tile_desc = reinterpret_cast<int32_t*>(base + l.tile_desc);
+  a.hist = reinterpret_cast<int32_t*>(base + l.hist);
   a.act = reinterpret_cast<uint16_t*>(base + l.act16);
   a.y = l.y16 ? reinterpret_cast<uint16_t*>(base + l.y16) : nullptr;
   a.scores = reinterpret_cast<const float*>(base + l.scores);

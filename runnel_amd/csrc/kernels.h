@@ -115,6 +115,7 @@ hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* partials,
 // ---- prefill (prefill.hip): expert-sorted grouped dequant-GEMM on MFMA.
 constexpr int kPrefillMaxExperts = 512;  // buckets of the one-workgroup sort
 constexpr int kPrefillBM = 128;          // sorted rows per m-tile (long prefill)
+constexpr int kPrefillMaxSlices = 64;   // sorting workgroups at most
 constexpr int kPrefillTileN = 128;       // [up; gate] pairs per gate/up tile
 constexpr int kPrefillMinRows = 64;      // (token, slot) rows that select it
 
@@ -128,6 +129,7 @@ struct PrefillArgs {
   int32_t* offs;           // [E + 3] rows per bucket (E: shared, E + 1: bad ids)
   int32_t* tile_offs;      // [E + 3] m-tiles per bucket; [E + 2] = total
   int32_t* tile_desc;      // [m-tiles][4]: bucket, first sorted row, rows, 0
+  int32_t* hist;           // [sort slices][E + 2] rows per bucket of each slice
   uint16_t* act;           // [T K + T, I] bf16, sorted order
   uint16_t* y;             // [T K (+ T), H] bf16 at row t K + j (shared: T K + t)
   const float* scores;     // [T, K + 1] router scores, slot K = shared gate
@@ -137,6 +139,7 @@ struct PrefillArgs {
 
 int prefill_tile_rows(int T, int K, int E);
 int prefill_max_mtiles(int T, int K, int E, int bm);
+int prefill_sort_slices(int T, int K);
 hipError_t launch_prefill(const PrefillArgs& a, int bits, bool combine, hipStream_t s);
 
 }  // namespace rmoe

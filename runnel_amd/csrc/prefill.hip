@@ -3,12 +3,14 @@
 // Used when a call routes at least 64 (token, slot) rows, the point where
 // the packed module sorts its rows by expert (src/runnel/mlx.py:59-63).
 //
-//   prefill_sort_kernel     one workgroup: stable counting sort of the
-//                           (token, slot) rows by expert id (mlx-lm
-//                           _gather_sort order), the shared expert's rows
-//                           appended as bucket E, out-of-range ids as
-//                           bucket E + 1; row and m-tile offsets per bucket
-//                           and one descriptor per m-tile.
+//   prefill_hist_kernel,    stable counting sort of the (token, slot) rows
+//   prefill_place_kernel    by expert id (mlx-lm _gather_sort order) over
+//                           slices of 2048 rows, one per workgroup: bucket
+//                           counts per slice, then every workgroup places
+//                           its rows; the shared expert's rows appended as
+//                           bucket E, out-of-range ids as bucket E + 1; row
+//                           and m-tile offsets per bucket and one
+//                           descriptor per m-tile.
 //   prefill_gemm_kernel     MODE 0 (gate/up): one (m-tile, n-tile of [up;
 //                           gate] pairs) per workgroup; the x rows of the
 //                           tile staged in LDS, every wave streams its own
@@ -49,6 +51,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kSortRowsPerSlice = 2048;  // rows per sorting workgroup
 constexpr int kPad = 8;                         // bf16 of padding per LDS row
 
 // K advances in chunks of KC values.  Each lane group g = l / 16 owns KC / 4
@@ -143,8 +146,45 @@ __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& 
 }  // namespace
 
 // ------------------------------------------------------------------- sort
-__global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const PrefillArgs p) {
+// Rows r = t K + j are cut into contiguous slices, one per workgroup, and
+// each slice into contiguous runs, one per wave: a row's place in its
+// bucket is (rows of the bucket in earlier slices) + (in earlier runs of
+// its slice) + (earlier in its run), so the order within a bucket is the
+// row order (stable).
+
+// This workgroup's slice [*r0, *r1) of the n rows.
+__device__ __forceinline__ void sort_slice(int n, int nw, int w, int& r0, int& r1) {
+  const int per = ((n + nw - 1) / nw + 63) & ~63;
+  r0 = min(n, w * per);
+  r1 = min(n, r0 + per);
+}
+
+__device__ __forceinline__ int bucket_of(const PrefillArgs& p, int r) {
+  const int e = p.idx[r];
+  return (unsigned)e < (unsigned)p.E ? e : p.E + 1;
+}
+
+// Pass 1: rows per bucket of each slice -> hist[slice][bucket].
+__global__ __launch_bounds__(kSortThreads) void prefill_hist_kernel(const PrefillArgs p) {
+  const int NB = p.E + 2;
+  __shared__ int s_hist[kPrefillMaxExperts + 2];
+  const int tid = threadIdx.x;
+  for (int b = tid; b < NB; b += kSortThreads) s_hist[b] = 0;
+  __syncthreads();
+  int r0, r1;
+  sort_slice(p.T * p.K, gridDim.x, blockIdx.x, r0, r1);
+  for (int r = r0 + tid; r < r1; r += kSortThreads) atomicAdd(&s_hist[bucket_of(p, r)], 1);
+  __syncthreads();
+  for (int b = tid; b < NB; b += kSortThreads) p.hist[blockIdx.x * NB + b] = s_hist[b];
+}
+
+// Pass 2: every workgroup scans the bucket totals itself (workgroup 0 also
+// publishes the offsets and the m-tile descriptors), then places the rows
+// of its slice.
+__global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const PrefillArgs p) {
   const int NB = p.E + 2;  // routed buckets, shared, out-of-range
+  const int NW = gridDim.x;
+  const int w = blockIdx.x;
   __shared__ int s_hist[kSortWaves * (kPrefillMaxExperts + 2)];
   __shared__ int s_scan[2][kSortThreads];
   __shared__ int s_shared_off;
@@ -152,27 +192,18 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
   const int wave = tid >> 6;
   const int lane = tid & 63;
   for (int i = tid; i < kSortWaves * NB; i += kSortThreads) s_hist[i] = 0;
-  __syncthreads();
 
-  const int n = p.T * p.K;
-  const int per = ((n + kSortWaves - 1) / kSortWaves + 63) & ~63;
-  const int r0 = min(n, wave * per);
-  const int r1 = min(n, r0 + per);
-  int* my = s_hist + wave * NB;
-  for (int r = r0 + lane; r < r1; r += 64) {
-    int e = p.idx[r];
-    e = (unsigned)e < (unsigned)p.E ? e : p.E + 1;
-    atomicAdd(&my[e], 1);
-  }
-  __syncthreads();
-
-  // Per bucket: total rows and m-tiles; exclusive scans over buckets.
-  int rows_b = 0, tiles_b = 0;
+  // Per bucket: total rows, rows in earlier slices, m-tiles.
+  int rows_b = 0, before_b = 0, tiles_b = 0;
   if (tid < NB) {
     if (tid == p.E) {
       rows_b = p.has_shared ? p.T : 0;
     } else {
-      for (int w = 0; w < kSortWaves; ++w) rows_b += s_hist[w * NB + tid];
+      for (int v = 0; v < NW; ++v) {
+        const int c = p.hist[v * NB + tid];
+        rows_b += c;
+        before_b += v < w ? c : 0;
+      }
     }
     tiles_b = (rows_b + p.bm - 1) / p.bm;
   }
@@ -187,27 +218,40 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
     s_scan[1][tid] += b;
     __syncthreads();
   }
+
+  // this workgroup's slice, one run per wave: per-wave counts
+  const int n = p.T * p.K;
+  int r0, r1;
+  sort_slice(n, NW, w, r0, r1);
+  const int per = ((r1 - r0 + kSortWaves - 1) / kSortWaves + 63) & ~63;
+  const int q0 = min(r1, r0 + wave * per);
+  const int q1 = min(r1, q0 + per);
+  int* my = s_hist + wave * NB;
+  for (int r = q0 + lane; r < q1; r += 64) atomicAdd(&my[bucket_of(p, r)], 1);
+  __syncthreads();
+
   if (tid < NB) {
     const int row_off = s_scan[0][tid] - rows_b;
-    p.offs[tid] = row_off;
-    p.tile_offs[tid] = s_scan[1][tid] - tiles_b;
-    if (tid == NB - 1) {
-      p.offs[NB] = s_scan[0][tid];
-      p.tile_offs[NB] = s_scan[1][tid];
-    }
-    // this bucket's m-tiles
     const int t0 = s_scan[1][tid] - tiles_b;
-    for (int i = 0; i < tiles_b; ++i) {
-      const int r = row_off + i * p.bm;
-      *reinterpret_cast<int4*>(p.tile_desc + 4 * (t0 + i)) =
-          make_int4(tid, r, min(p.bm, row_off + rows_b - r), 0);
+    if (w == 0) {
+      p.offs[tid] = row_off;
+      p.tile_offs[tid] = t0;
+      if (tid == NB - 1) {
+        p.offs[NB] = s_scan[0][tid];
+        p.tile_offs[NB] = s_scan[1][tid];
+      }
+      for (int i = 0; i < tiles_b; ++i) {
+        const int r = row_off + i * p.bm;
+        *reinterpret_cast<int4*>(p.tile_desc + 4 * (t0 + i)) =
+            make_int4(tid, r, min(p.bm, row_off + rows_b - r), 0);
+      }
     }
-    // per-wave bases of this bucket (stable: wave order = row order)
-    int base = row_off;
+    // per-wave bases of this bucket in this slice
+    int base = row_off + before_b;
     if (tid != p.E) {
-      for (int w = 0; w < kSortWaves; ++w) {
-        const int c = s_hist[w * NB + tid];
-        s_hist[w * NB + tid] = base;
+      for (int v = 0; v < kSortWaves; ++v) {
+        const int c = s_hist[v * NB + tid];
+        s_hist[v * NB + tid] = base;
         base += c;
       }
     } else {
@@ -216,18 +260,15 @@ __global__ __launch_bounds__(kSortThreads) void prefill_sort_kernel(const Prefil
   }
   __syncthreads();
   if (p.has_shared)
-    for (int t = tid; t < p.T; t += kSortThreads) p.rows[s_shared_off + t] = n + t;
+    for (int t = w * kSortThreads + tid; t < p.T; t += NW * kSortThreads)
+      p.rows[s_shared_off + t] = n + t;
 
-  // Stable ranking: each wave walks its rows in order, 64 at a time; the
+  // Stable ranking: each wave walks its run in order, 64 at a time; the
   // lanes holding one bucket find each other with one ballot per id bit.
-  for (int c0 = r0; c0 < r1; c0 += 64) {
+  for (int c0 = q0; c0 < q1; c0 += 64) {
     const int r = c0 + lane;
-    const bool v = r < r1;
-    int e = 0;
-    if (v) {
-      e = p.idx[r];
-      e = (unsigned)e < (unsigned)p.E ? e : p.E + 1;
-    }
+    const bool v = r < q1;
+    const int e = v ? bucket_of(p, r) : 0;
     uint64_t mask = __ballot(v);
 #pragma unroll
     for (int b = 0; b < 10; ++b) {
@@ -640,6 +681,12 @@ int prefill_tile_rows(int T, int K, int E) {
   return (long)T * K <= 48L * E ? 32 : kPrefillBM;
 }
 
+int prefill_sort_slices(int T, int K) {
+  const long n = (long)T * K;
+  const long nw = (n + kSortRowsPerSlice - 1) / kSortRowsPerSlice;
+  return (int)(nw < 1 ? 1 : nw > kPrefillMaxSlices ? kPrefillMaxSlices : nw);
+}
+
 int prefill_max_mtiles(int T, int K, int E, int bm) {
   return (T * K + T + bm - 1) / bm + E + 2;
 }
@@ -661,7 +708,9 @@ void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
 hipError_t launch_prefill(const PrefillArgs& args, int bits, bool combine, hipStream_t s) {
   PrefillArgs a = args;
   a.bm = prefill_tile_rows(a.T, a.K, a.E);
-  hipLaunchKernelGGL(prefill_sort_kernel, dim3(1), dim3(kSortThreads), 0, s, a);
+  const int nw = prefill_sort_slices(a.T, a.K);
+  hipLaunchKernelGGL(prefill_hist_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
+  hipLaunchKernelGGL(prefill_place_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
   const int mt = prefill_max_mtiles(a.T, a.K, a.E, a.bm);
   if (bits == 8) {
     if (a.bm == 32) launch_gemms<8, 32>(a, mt, s);
