@@ -175,7 +175,7 @@ typedef float f32x4_r __attribute__((ext_vector_type(4)));
 // One wave: 16 tokens x 64 experts, K in chunks of 64 (four chunks of
 // loads in flight per lane); lane (col, g) holds A row / B column `col` and
 // k = 16 g + [0, 16) of each chunk.
-__global__ __launch_bounds__(64) void router_logits_mfma_kernel(const DecodeArgs p) {
+__global__ __launch_bounds__(64) void router_logits16_kernel(const DecodeArgs p) {
   const int lane = threadIdx.x;
   const int col = lane & 15;
   const int g = lane >> 4;
@@ -219,6 +219,74 @@ __global__ __launch_bounds__(64) void router_logits_mfma_kernel(const DecodeArgs
       if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col] = acc[cb][i];
     }
 }
+
+// Long prefills: one wave takes 64 tokens x 64 experts (4 x 4 MFMA tiles),
+// so each router row is read once per 64 tokens; K in chunks of 64 with the
+// next chunk's loads in flight, same lane layout.
+__global__ __launch_bounds__(64) void router_logits64_kernel(const DecodeArgs p) {
+  constexpr int kRouterTB = 4;  // 16-token blocks per wave
+  const int lane = threadIdx.x;
+  const int col = lane & 15;
+  const int g = lane >> 4;
+  const int t0 = blockIdx.x * 16 * kRouterTB;
+  const int e0 = blockIdx.y * 64;
+  const uint16_t* xa[kRouterTB];
+#pragma unroll
+  for (int tb = 0; tb < kRouterTB; ++tb)
+    xa[tb] = p.x + (size_t)min(t0 + tb * 16 + col, p.T - 1) * p.H + g * 16;
+  const uint16_t* wb[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) wb[cb] = p.router_w + (size_t)(e0 + cb * 16 + col) * p.H + g * 16;
+  f32x4_r acc[kRouterTB][4];
+#pragma unroll
+  for (int tb = 0; tb < kRouterTB; ++tb)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+  auto load = [&](int c, u32x4 (&a)[kRouterTB][2], u32x4 (&b)[4][2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int tb = 0; tb < kRouterTB; ++tb)
+        a[tb][j] = *reinterpret_cast<const u32x4*>(xa[tb] + c * 64 + 8 * j);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        b[cb][j] = *reinterpret_cast<const u32x4*>(wb[cb] + c * 64 + 8 * j);
+    }
+  };
+  const int nch = p.H / 64;
+  u32x4 a[kRouterTB][2], b[4][2];
+  load(0, a, b);
+  for (int c = 0; c < nch; ++c) {
+    u32x4 na[kRouterTB][2], nb[4][2];
+    load(min(c + 1, nch - 1), na, nb);  // the last chunk loads itself again
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int tb = 0; tb < kRouterTB; ++tb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          acc[tb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_r, a[tb][j]), __builtin_bit_cast(bf16x8_r, b[cb][j]),
+              acc[tb][cb], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int tb = 0; tb < kRouterTB; ++tb) a[tb][j] = na[tb][j];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) b[cb][j] = nb[cb][j];
+    }
+  }
+#pragma unroll
+  for (int tb = 0; tb < kRouterTB; ++tb)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + tb * 16 + 4 * g + i;
+        if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col] = acc[tb][cb][i];
+      }
+}
+
 
 // The router contract's dot of one token row (held as xv, chunk lane + 64 c
 // per lane) with one weight row.
@@ -630,8 +698,12 @@ bool router_mfma_eligible(int E, int H) {
 
 hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, hipStream_t s) {
   hipLaunchKernelGGL(router_rownorm_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, wnorm);
-  hipLaunchKernelGGL(router_logits_mfma_kernel, dim3((a.T + 15) / 16, a.E / 64), dim3(64), 0,
-                     s, a);
+  if (a.T >= 4096)
+    hipLaunchKernelGGL(router_logits64_kernel, dim3((a.T + 63) / 64, a.E / 64), dim3(64), 0, s,
+                       a);
+  else
+    hipLaunchKernelGGL(router_logits16_kernel, dim3((a.T + 15) / 16, a.E / 64), dim3(64), 0, s,
+                       a);
   hipLaunchKernelGGL(router_select_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                      (const float*)wnorm);
   RMOE_CHECK_LAUNCH();
