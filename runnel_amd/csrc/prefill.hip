@@ -540,30 +540,47 @@ struct Gemm {
     if (ch < nch) step<MBA, 0>(ch, nch, asrc, live, ar, bw, bs, bb, acc);
   }
 
+  // The tile's bf16 outputs go through LDS (the A buffers, free once every
+  // wave has finished its last chunk) so that each row leaves in 16-byte
+  // pieces: act rows (SwiGLU) in sorted order, or y rows at their (token,
+  // slot) place.
   __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
+    constexpr int OS = TN + 8;  // LDS row stride (bf16)
+    static_assert(BM * OS <= 2 * BM * C::ROW, "output tile fits in the A buffers");
+    uint16_t* so = &s_a[0][0];
+    __syncthreads();
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       if (mb >= mba) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = mb * 16 + kg * 4 + i;
-        if (r >= tile.nrows) continue;
         if constexpr (MODE == 0) {
 #pragma unroll
           for (int h = 0; h < QPW / 2; ++h) {
-            const int c = tile.n * TN + wave * (8 * QPW) + h * 16 + col_l;
+            const int c = wave * (8 * QPW) + h * 16 + col_l;
             const float up = round_bf16(acc[mb][h][i]);
             const float gate = round_bf16(acc[mb][QPW / 2 + h][i]);
-            p.act[(size_t)(tile.row0 + r) * p.I + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
+            so[r * OS + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
           }
         } else {
 #pragma unroll
           for (int qq = 0; qq < QPW; ++qq) {
-            const int c = tile.n * TN + wave * (16 * QPW) + qq * 16 + col_l;
-            p.y[(size_t)s_row[r] * p.H + c] = (uint16_t)f32_to_bf16(acc[mb][qq][i]);
+            const int c = wave * (16 * QPW) + qq * 16 + col_l;
+            so[r * OS + c] = (uint16_t)f32_to_bf16(acc[mb][qq][i]);
           }
         }
       }
+    }
+    __syncthreads();
+    constexpr int PR = TN / 8;  // 16-byte pieces per row
+    for (int pi = tid; pi < tile.nrows * PR; pi += THREADS) {
+      const int r = pi / PR;
+      const int c8 = pi - r * PR;
+      const uint4 v = *reinterpret_cast<const uint4*>(so + r * OS + c8 * 8);
+      uint16_t* dst = MODE == 0 ? p.act + (size_t)(tile.row0 + r) * p.I
+                                : p.y + (size_t)s_row[r] * p.H;
+      *reinterpret_cast<uint4*>(dst + tile.n * TN + c8 * 8) = v;
     }
   }
 };
