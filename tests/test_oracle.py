@@ -214,3 +214,50 @@ def test_gather_sort_permutation():
     for e in np.unique(flat):
         pos = order[sorted_e == e]
         assert np.all(np.diff(pos) > 0)
+
+
+# ---- prefill contract (mode="prefill": weights rounded to bf16 first)
+
+def test_prefill_weight_rounding_is_nearest_even():
+    """Halfway cases pin round-to-nearest-even (truncation or round-half-up
+    both fail): bf16 spacing at 1 is 2^-7."""
+    v = np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, -(1 + 3 * 2.0 ** -8), 1 + 2.0 ** -9,
+                  1 + 2.0 ** -8 + 2.0 ** -20])
+    got = M._bf16_weights(v)
+    assert got.tolist() == [1.0, 1 + 2.0 ** -6, -(1 + 2.0 ** -6), 1.0, 1 + 2.0 ** -7]
+
+
+def _exact_affine(q: M.QWeight):
+    """Scales 2^-6 and biases -2^-3 everywhere: every q*s + b = (q - 8)/64
+    has at most 8 significant bits, so bf16 holds it exactly."""
+    q.scales[...] = M.f32_to_bf16(np.float32(2.0 ** -6))
+    q.biases[...] = M.f32_to_bf16(np.float32(-0.125))
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_prefill_mode_equals_contract_when_weights_are_bf16(bits):
+    """Closed form: with bf16-representable dequantised weights the weight
+    rounding is the identity, so the prefill contract is the decode contract
+    bit for bit (a dropped or misplaced rounding elsewhere would differ)."""
+    L = M.make_layer(21, hidden=256, inter=128, experts=8, top_k=2, bits=bits)
+    for q in (L.gate_up, L.down, L.shared_gate_up, L.shared_down):
+        _exact_affine(q)
+    x = M.make_x(22, 6, 256)
+    a, ia, _ = M.block_forward(L, x, mode="contract")
+    b, ib, _ = M.block_forward(L, x, mode="prefill")
+    assert np.array_equal(ia, ib)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_prefill_mode_close_to_contract(bits):
+    """On ordinary layers the two contracts differ only by the weight
+    rounding (relative 2^-9 per weight): outputs agree to a few bf16 steps
+    and are not identical (the rounding is really applied)."""
+    L = M.make_layer(23, hidden=256, inter=128, experts=8, top_k=2, bits=bits)
+    x = M.make_x(24, 6, 256)
+    a, _, _ = M.block_forward(L, x, mode="contract")
+    b, _, _ = M.block_forward(L, x, mode="prefill")
+    fa, fb = M.bf16_to_f32(a), M.bf16_to_f32(b)
+    assert not np.array_equal(a, b)
+    assert np.abs(fa - fb).max() <= 4 * 2.0 ** -8 * max(np.abs(fa).max(), 1e-3)
