@@ -276,6 +276,8 @@ bool fused_eligible(const rmoe_layer* L, int* grid) {
   int g = 0;
   if (rmoe::fused_grid(L->gate_up.bits, &g) != hipSuccess) return false;
   const int waves = g * (rmoe::kFusedThreads / 64);
+  // the router rows are computed once per XCD by its g / 8 workgroups
+  if (g % 8 != 0 || g < L->experts) return false;
   if (waves < rmoe::kFusedH * 1 / rmoe::kMaxFusedRowsPerWave) return false;
   if ((units * rmoe::kFusedI + waves - 1) / waves > rmoe::kMaxFusedPairsPerWave) return false;
   // every workgroup must own at least one gate/up pair (the epoch hand-over

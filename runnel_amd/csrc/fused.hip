@@ -4,10 +4,14 @@
 // workgroup is resident (inside a captured graph: a plain launch of the same
 // grid, see launch_fused_decode).  Per layer:
 //
-//   R  router rows, one per workgroup (the fixed-order dot of the router
-//      contract); the row weights are loaded before x is even staged
-//   K  every workgroup ranks all logits itself: 4 keys per lane sorted
-//      locally, then top_k rounds of a DPP wave maximum
+//   R  router rows: the waves of each XCD compute every router row once
+//      (the fixed-order dot of the router contract) and publish it in that
+//      XCD's L2 only; the row weights are loaded before x is even staged
+//   K  every workgroup polls its XCD's logits (an L2 round trip, about half
+//      the latency of the device-coherent hand-overs) and ranks them with the
+//      shared gate's logit, which its wave 0 computes itself (row weights
+//      prefetched like the router rows): 4 keys per lane sorted locally, then
+//      top_k rounds of a DPP wave maximum
 //   G  gate/up pairs: every wave issues the loads of all its pairs and of
 //      its down row of every unit at once (about 110 KB per CU in flight),
 //      computes SwiGLU
@@ -39,7 +43,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kSpinLimit = 1 << 20;
 // Waves that collect the hand-overs for their workgroup: router rows and
 // shared-expert pairs (prefetched for the next layer) sit on waves 0 and 1.
-constexpr int kPollWave = kWaves - 1;  // logits
+constexpr int kPollWave = 0;  // logits: a wave that polls neither x nor act
 constexpr int kXPollWaves = 4;         // x: waves 4..7
 constexpr int kActPollWaves = 6;       // act: waves 2..7
 
@@ -56,6 +60,11 @@ __device__ __forceinline__ uint32_t tagged(uint32_t bf16_bits, uint32_t tag) {
 __device__ __forceinline__ bool tag_ok(uint32_t word, uint32_t tag) {
   return (word & 0xFFFFu) == (tag & 0xFFFFu);
 }
+// XCD-local hand-over (workgroup i runs on XCD i % 8): stores reach the
+// XCD's L2 (the vector L1 writes through); loads with sc0 nt skip the L1
+// and are served by that L2.  Only valid between workgroups of one XCD.
+constexpr int kXcdLoadAux = 3;   // sc0 | nt
+constexpr int kXcdStoreAux = 1;  // sc0
 
 // Wave maximum of unsigned keys with the DPP pattern of wave_sum; the
 // result is uniform.
@@ -252,13 +261,18 @@ __device__ __forceinline__ void issue_fence() {
 template <int BITS, int RC>
 __device__ __forceinline__ void issue_router_and_shared_down(
     const FusedLayer& L, int row, int n_rows, int E, bool has_shared, int h, int lane,
-    uint4 (&rw)[RC], DownRegs<Shape<BITS>::DN_WPL>& drs, uint32_t& dpws) {
+    bool sg_wave, uint4 (&rw)[RC], uint4 (&sw)[RC], DownRegs<Shape<BITS>::DN_WPL>& drs,
+    uint32_t& dpws) {
   using S = Shape<BITS>;
   constexpr int H = S::H;
   if (row < n_rows) {
     const uint16_t* wr = row < E ? L.router_w + (size_t)row * H : L.sgate_w;
 #pragma unroll
     for (int i = 0; i < RC; ++i) rw[i] = load16_stream(wr + (lane + 64 * i) * 8);
+  }
+  if (sg_wave && has_shared && L.sgate_w) {
+#pragma unroll
+    for (int i = 0; i < RC; ++i) sw[i] = load16_stream(L.sgate_w + (lane + 64 * i) * 8);
   }
   if (has_shared && h < H) {
     if (lane < 8) dpws = load_down_param_word<BITS>(L.sdn, h, lane);
@@ -314,7 +328,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   const int U = K + p.has_shared;
   const int n_pairs = U * I;
   const int h = gwave;            // one down row per wave (n_waves >= H is checked)
-  const int row = wg + G * wave;  // router row of this wave, if any
+  const int xcd = wg & 7;
+  // router row of this wave within its XCD (G / 8 workgroups x 8 waves >= E
+  // is checked), if any; the shared gate's row is done by every workgroup
+  const int row = (wg >> 3) + (G >> 3) * wave;
   // gate/up pairs q = pw + pp * n_waves: the pairs past 2 * n_waves land on
   // low wave indices of every workgroup, so each CU streams the same bytes
   const int pw = wg + G * wave;
@@ -336,12 +353,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   PairRegs<CPL> pr[NP];
   DownRegs<S::DN_WPL> dr[NU];      // slot NU-1: the shared unit
   uint32_t dpw0 = 0, dpw1 = 0;
-  uint4 rw[RC];
+  uint4 rw[RC], sw[RC];  // router row; shared gate row (wave kPollWave)
   {
     const FusedLayer L0 = p.table ? p.table[0] : p.layer0;
-    const int n_rows0 = E + ((p.has_shared && L0.sgate_w) ? 1 : 0);
-    issue_router_and_shared_down<BITS, RC>(L0, row, n_rows0, E, p.has_shared, h, lane0, rw,
-                                           dr[NU - 1], dpw1);
+    issue_router_and_shared_down<BITS, RC>(L0, row, E, E, p.has_shared, h, lane0,
+                                           wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
     issue_shared_pairs<BITS, CPL, NP>(L0, p.has_shared, K, pw, n_waves, n_pairs, lane0, pr);
   }
   __syncthreads();
@@ -363,7 +379,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     const uint32_t tag_x = base + phase + 3;  // used when a next layer reads x
     phase += last ? 2 : 3;
     const bool sg_row = p.has_shared && L.sgate_w;
-    const int n_rows = E + (sg_row ? 1 : 0);
 
     // ---- x (bf16 -> fp32 in LDS).  A chained layer collects the previous
     // layer's tagged output.
@@ -378,7 +393,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     __syncthreads();
 
     // ---- R: this wave's router row.
-    if (row < n_rows) {
+    if (row < E) {
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < RC; ++i) {
@@ -393,29 +408,46 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         acc = fmaf(xv[7], bf16_hi(rw[i].w), acc);
       }
       acc = wave_sum(acc);
-      if (lane == 0) store_coherent_u32(sc->logits + row, tagged(f32_to_bf16(acc), tag_logit));
+      if (lane == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(
+            tagged(f32_to_bf16(acc), tag_logit),
+            __builtin_amdgcn_make_buffer_rsrc(sc->logits[xcd], (short)0, E * 4, 0x00020000),
+            row * 4, 0, kXcdStoreAux);
     }
 
     // ---- K: poll all logits (wave 0), rank them, publish in LDS.
     if (wave == kPollWave) {
-      // lane l holds experts 4 l .. 4 l + 3 (one 16-byte coherent load)
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          sc->logits, (short)0, (E + 1) * 4, 0x00020000);
-      uint32_t w[kPer];
+      // the shared gate's logit, computed here (its row is not handed over)
       uint32_t wsg = 0;
+      if (sg_row) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RC; ++i) {
+          const float* xv = s_x + (lane + 64 * i) * 8;
+          acc = fmaf(xv[0], bf16_lo(sw[i].x), acc);
+          acc = fmaf(xv[1], bf16_hi(sw[i].x), acc);
+          acc = fmaf(xv[2], bf16_lo(sw[i].y), acc);
+          acc = fmaf(xv[3], bf16_hi(sw[i].y), acc);
+          acc = fmaf(xv[4], bf16_lo(sw[i].z), acc);
+          acc = fmaf(xv[5], bf16_hi(sw[i].z), acc);
+          acc = fmaf(xv[6], bf16_lo(sw[i].w), acc);
+          acc = fmaf(xv[7], bf16_hi(sw[i].w), acc);
+        }
+        wsg = f32_to_bf16(wave_sum(acc)) << 16;
+      }
+      // lane l holds experts 4 l .. 4 l + 3 (one 16-byte load from the L2)
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          sc->logits[xcd], (short)0, E * 4, 0x00020000);
+      uint32_t w[kPer];
       for (int spin = 0;; ++spin) {
         bool ok = true;
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, 0, 16);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, 0, kXcdLoadAux);
         w[0] = v.x;
         w[1] = v.y;
         w[2] = v.z;
         w[3] = v.w;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) ok &= 4 * lane + i >= E || tag_ok(w[i], tag_logit);
-        if (sg_row && lane == 0) {
-          wsg = load_coherent_u32(sc->logits + E);
-          ok &= tag_ok(wsg, tag_logit);
-        }
         if (__all(ok)) break;
         if (spin >= kSpinLimit) { timed_out = true; break; }
         __builtin_amdgcn_s_sleep(1);
@@ -632,13 +664,12 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     // The next layer's routing-independent loads go out now that this
     // layer's down rows are done: issued earlier they would sit in front of
     // the hand-over polls of their wave (a wave's loads return in order).
-    // The polls use waves that carry the fewest of them (x: waves 4-7, act:
-    // 2-7, logits: 7; router rows and shared pairs sit on waves 0 and 1).
+    // x is polled by waves 4-7 and act by 2-7; the logits by wave 0, whose
+    // extra loads (shared gate row, shared pairs) are back by then.
     if (!last) {
       const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
-      const int n_rows_n = E + ((p.has_shared && Ln.sgate_w) ? 1 : 0);
-      issue_router_and_shared_down<BITS, RC>(Ln, row, n_rows_n, E, p.has_shared, h, lane, rw,
-                                             dr[NU - 1], dpw1);
+      issue_router_and_shared_down<BITS, RC>(Ln, row, E, E, p.has_shared, h, lane,
+                                             wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
       issue_shared_pairs<BITS, CPL, NP>(Ln, p.has_shared, K, pw, n_waves, n_pairs, lane, pr);
     }
     // s_x / s_act / s_idx are rewritten by the next layer

@@ -75,7 +75,7 @@ struct FusedScratch {
   uint32_t epoch;
   uint32_t err;
   uint32_t pad[62];
-  uint32_t logits[kFusedMaxExperts + 64];
+  uint32_t logits[8][kFusedMaxExperts];   // one copy per XCD (written and read there)
   uint32_t act[kMaxFusedUnits * kFusedI];
   uint32_t xs[2][kFusedH];
 };
