@@ -535,9 +535,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       if (q < n_pairs && u < K)
         load_pair_words<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
     }
-#pragma unroll
-    for (int u = 0; u < NU - 1; ++u)
-      if (u < K && h < H) load_down_words<BITS>(dr[u], L.dn, (size_t)s_idx[u] * H + h, lane);
     issue_fence();
 
     // ---- G: gate/up + SwiGLU of this wave's pairs -> tagged act words.
@@ -584,6 +581,14 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       // being hoisted (and spilled) while this one is reduced
       __builtin_amdgcn_sched_barrier(0);
     }
+
+    // ---- this wave's down row of every routed unit: issued after the
+    // gate/up math, so the gate/up rows have the memory system to themselves
+    // first; they land while the activations are handed over.
+#pragma unroll
+    for (int u = 0; u < NU - 1; ++u)
+      if (u < K && h < H) load_down_words<BITS>(dr[u], L.dn, (size_t)s_idx[u] * H + h, lane);
+    issue_fence();
 
     // ---- down scales / biases of every unit, ready before act arrives.
     const int gd = lane >> 3;
