@@ -339,7 +339,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 
   __shared__ float s_x[H];
   __shared__ float s_act[NU * I];
-  __shared__ float s_asum[NU * 64];
   __shared__ int s_idx[NU];
   __shared__ float s_coef[NU];
   __shared__ uint32_t s_base;
@@ -604,13 +603,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       poll_tagged<NU * I / 256 / kActPollWaves>(sc->act, n_pairs, tag_act, s_act, lane,
                                                 wave - (kWaves - kActPollWaves), timed_out);
     __syncthreads();
-    // sum of act over each lane's 8 values of each unit, shared by all waves
-    for (int i = threadIdx.x; i < U * 64; i += kThreads) {
-      const float4 a0 = *reinterpret_cast<const float4*>(s_act + i * 8);
-      const float4 a1 = *reinterpret_cast<const float4*>(s_act + i * 8 + 4);
-      s_asum[i] = ((((((a0.x + a0.y) + a0.z) + a0.w) + a1.x) + a1.y) + a1.z) + a1.w;
-    }
-    __syncthreads();
 
     // ---- D: down row h of every unit from registers.
     if (h < H) {
@@ -625,7 +617,9 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         const float4 a0 = *reinterpret_cast<const float4*>(s_act + u * I + lane * 8);
         const float4 a1 = *reinterpret_cast<const float4*>(s_act + u * I + lane * 8 + 4);
         const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        const float asum = s_asum[u * 64 + lane];
+        // sum of the lane's 8 activations (the group-affine bias term)
+        const float asum =
+            ((((((a0.x + a0.y) + a0.z) + a0.w) + a1.x) + a1.y) + a1.z) + a1.w;
         float qa = 0.0f;
         if constexpr (BITS == 8) {
           qa = qdot_word8(dr[uu].w[0], a[0], a[1], a[2], a[3], qa);
