@@ -77,14 +77,16 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t v, int ctrl) {
   }
 }
 __device__ __forceinline__ uint32_t wave_max_fast(uint32_t v) {
+  // rows of 16 by DPP, then across row pairs and halves with the gfx950
+  // permlane swaps (VALU, no LDS round trip): every lane ends with the max
   v = max(v, dpp_u(v, 0xB1));
   v = max(v, dpp_u(v, 0x4E));
   v = max(v, dpp_u(v, 0x141));
   v = max(v, dpp_u(v, 0x140));
-  v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));
-  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
-  return a > b ? a : b;
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(b[0], b[1]);
 }
 // One wave collects n_words tagged words written by other workgroups: 16-byte
 // loads at agent coherence (sc1, the bits agent-scope atomic loads use; each
