@@ -70,6 +70,9 @@ struct Chunk {
   static constexpr int LANE_WORDS = WORDS / 4;         // u32 per lane per row
   static constexpr int LPC = LANE_WORDS / 4;           // 16-byte loads per lane per row
   static constexpr int ROW = KC + kPad;                // LDS row (bf16)
+  // A stages in LDS: down (K = I, short) keeps up to four chunks, the whole
+  // K of I = 512, resident; gate/up double-buffers
+  static constexpr int STAGES = MODE == 1 ? 4 : 2;
   static constexpr int PIECES = BM * KC / 8;           // 16-byte A pieces
   static constexpr int PPT = PIECES / THREADS;         // pieces per thread
   static_assert(PIECES % THREADS == 0, "A tile must split evenly");
@@ -305,7 +308,7 @@ struct Gemm {
 
   const PrefillArgs& p;
   const Tile& tile;
-  uint16_t (*s_a)[BM * C::ROW];
+  uint16_t (*s_a)[BM * C::ROW];  // [C::STAGES]
   const int* s_row;
   int tid, wave, lane, col_l, kg, K;
   QW q;
@@ -513,8 +516,43 @@ struct Gemm {
     }
   }
 
+  // Down with K <= STAGES chunks: every A chunk is loaded and stored once up
+  // front (one barrier for the whole tile); weights stream two chunks ahead.
+  template <int MBA>
+  __device__ void run_full(f32x4_t (&acc)[MB][QPW]) const {
+    const int nch = K / C::KC;
+    const uint16_t* asrc[C::PPT];
+    bool live[C::PPT];
+    a_rows(asrc, live);
+    uint4 bw[2][QPW][C::LPC];
+    uint32_t bs[2][QPW], bb[2][QPW];
+    uint4 ar[C::STAGES][C::PPT];
+#pragma unroll
+    for (int c = 0; c < C::STAGES; ++c)
+      if (BM == 32 ? (c < nch) : true) load_a_live(min(c, nch - 1), asrc, live, ar[c]);
+    load_b(0, bw[0], bs[0], bb[0]);
+    load_b(min(1, nch - 1), bw[1], bs[1], bb[1]);
+#pragma unroll
+    for (int c = 0; c < C::STAGES; ++c)
+      if (c < nch) store_a(c, ar[c], live);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < C::STAGES; ++c) {
+      if (c >= nch) break;
+      const int S = c & 1;
+      chunk<MBA>(c, bw[S], bs[S], bb[S], acc);
+      load_b(min(c + 2, nch - 1), bw[S], bs[S], bb[S]);
+    }
+  }
+
   template <int MBA>
   __device__ void run(f32x4_t (&acc)[MB][QPW]) const {
+    if constexpr (MODE == 1) {
+      if (K <= C::STAGES * C::KC) {
+        run_full<MBA>(acc);
+        return;
+      }
+    }
     if constexpr (BM == 32) {
       run1<MBA>(acc);
       return;
@@ -546,7 +584,7 @@ struct Gemm {
   // slot) place.
   __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
     constexpr int OS = TN + 8;  // LDS row stride (bf16)
-    static_assert(BM * OS <= 2 * BM * C::ROW, "output tile fits in the A buffers");
+    static_assert(BM * OS <= C::STAGES * BM * C::ROW, "output tile fits in the A buffers");
     uint16_t* so = &s_a[0][0];
     __syncthreads();
 #pragma unroll
@@ -591,7 +629,7 @@ __attribute__((amdgpu_waves_per_eu(Chunk<BITS, BM, MODE>::MIN_WAVES))) void pref
     const PrefillArgs p,
                                                                      const int nt) {
   using G = Gemm<BITS, BM, MODE>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * G::C::ROW];
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[G::C::STAGES][BM * G::C::ROW];
   __shared__ int s_row[BM];
   Tile tile;
   if (!decode_tile(p, nt, tile)) return;
