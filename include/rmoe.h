@@ -30,6 +30,8 @@
  *                     bench/mlx_component_profile.py:130)
  *   rmoe_router       the router half of that block (gate -> softmax ->
  *                     top-k -> renormalise)
+ *   rmoe_router_q     the same with the 8-bit QuantizedLinear gate of real
+ *                     checkpoints (bench/runnel_bench/checkpoint.py:200-208)
  *   rmoe_quantize / rmoe_dequantize
  *                     mx.quantize / mx.dequantize (affine, group 64), the
  *                     format produced for the banks that
@@ -47,7 +49,7 @@
 extern "C" {
 #endif
 
-#define RMOE_ABI_VERSION 1
+#define RMOE_ABI_VERSION 2
 
 #define RMOE_OK 0
 #define RMOE_EINVAL (-1) /* inconsistent or unsupported shape / argument */
@@ -73,7 +75,17 @@ typedef struct rmoe_qweight {
 /* One MoE layer's resident weights.  gate_up rows are [up; gate]
  * (src/runnel/mlx.py:38-48).  The shared expert is present when
  * shared_gate_up.w != NULL; shared_gate_w (bf16 [hidden]) is its sigmoid
- * gate.  norm_topk_prob != 0 renormalises the selected probabilities. */
+ * gate.  norm_topk_prob != 0 renormalises the selected probabilities.
+ *
+ * The router gate is either bf16 (router_w) or an 8-bit group-64 MLX-affine
+ * bank (router_q, [1, experts, hidden]; router_w NULL), the format real
+ * checkpoints give mlp.gate and mlp.shared_expert_gate
+ * (bench/runnel_bench/checkpoint.py:200-208,
+ * bench/results/m0/checkpoint-ornith-mlx-8bit.json:163-175).  The shared
+ * gate then uses the same format: shared_gate_q [1, 1, hidden] instead of
+ * shared_gate_w.  Quantized gate logits follow a fixed fp32 order of their
+ * own: 16-code chunks lane + 64 i of a 64-lane wave, per chunk
+ * acc = fma(sum q x, s, acc), acc = fma(sum x, b, acc), then a butterfly. */
 typedef struct rmoe_layer {
   int32_t hidden;
   int32_t inter;
@@ -87,6 +99,8 @@ typedef struct rmoe_layer {
   rmoe_qweight down;             /* [experts, hidden, inter] */
   rmoe_qweight shared_gate_up;   /* [1, 2*shared_inter, hidden] */
   rmoe_qweight shared_down;      /* [1, hidden, shared_inter] */
+  rmoe_qweight router_q;         /* 8-bit gate [1, experts, hidden], or w NULL */
+  rmoe_qweight shared_gate_q;    /* 8-bit shared gate [1, 1, hidden], or w NULL */
 } rmoe_layer;
 
 int rmoe_abi_version(void);
@@ -110,6 +124,14 @@ int rmoe_router(const uint16_t* router_w, int32_t experts, int32_t hidden,
                 void* workspace, size_t workspace_bytes, void* stream);
 size_t rmoe_router_workspace_bytes(int32_t experts, int32_t top_k,
                                    int32_t tokens);
+
+/* The same router with an 8-bit group-64 quantized gate (mlx-lm's
+ * QuantizedLinear gate, x @ dequantize(W)^T): router [1, experts, hidden]
+ * (experts = router->rows, hidden = router->cols), logits in the quantized
+ * gate's fixed fp32 order.  Workspace: rmoe_router_workspace_bytes. */
+int rmoe_router_q(const rmoe_qweight* router, int32_t top_k, int32_t norm_topk_prob,
+                  const uint16_t* x, int32_t tokens, int32_t* indices, float* scores,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* FusedQuantizedSwitchGLU.__call__ (src/runnel/mlx.py:57-82): for every
  * (token, slot) the packed [up; gate] projection of expert indices[t, j],

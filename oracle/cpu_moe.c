@@ -338,6 +338,10 @@ typedef struct {
   orc_qweight down;              /* [experts, hidden, inter] */
   orc_qweight shared_gate_up;    /* [1, 2*shared_inter, hidden] or w == NULL */
   orc_qweight shared_down;       /* [1, hidden, shared_inter] */
+  orc_qweight router_q;          /* quantized gate [1, experts, hidden], used
+                                    when router_w is NULL */
+  orc_qweight shared_gate_q;     /* quantized shared gate [1, 1, hidden], used
+                                    when shared_gate_w is NULL and w != NULL */
 } orc_layer;
 
 /*
@@ -365,6 +369,52 @@ float orc_router_dot(const uint16_t* x, const uint16_t* w, int hidden) {
     memcpy(p, q, sizeof(p));
   }
   return p[0];
+}
+
+/*
+ * Quantized gate (MLX affine, group 64) row dot in the GPU router's fixed
+ * order.  The codes are cut into 16-byte chunks of V = 128 / bits values;
+ * lane l of 64 takes chunks l, l+64, ... from acc = +0: per chunk
+ * qa = sum q_i x_i and xs = sum x_i, each sequential from +0 (the products
+ * are exact in fp32), then acc = fmaf(qa, s, acc), acc = fmaf(xs, b, acc)
+ * with the chunk's group scale and bias; the lane sums are combined by the
+ * butterfly of orc_router_dot.
+ */
+float orc_qrouter_dot(const orc_qweight* qw, int row, const uint16_t* x) {
+  const int H = qw->cols, bits = qw->bits, V = 128 / bits;
+  const size_t stride = (size_t)H / values_per_word(bits);
+  const size_t groups = (size_t)H / (size_t)qw->group;
+  const uint32_t* words = qw->w + (size_t)row * stride;
+  const int chunks = H / V;
+  float p[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int c = l; c < chunks; c += 64) {
+      float qa = 0.0f, xs = 0.0f;
+      for (int i = 0; i < V; ++i) {
+        const size_t k = (size_t)c * V + (size_t)i;
+        const float xv = orc_bf16_to_f32(x[k]);
+        qa += (float)unpack_q(words, k, bits) * xv;
+        xs += xv;
+      }
+      const size_t g = (size_t)row * groups + (size_t)c * V / (size_t)qw->group;
+      acc = fmaf(qa, orc_bf16_to_f32(qw->scales[g]), acc);
+      acc = fmaf(xs, orc_bf16_to_f32(qw->biases[g]), acc);
+    }
+    p[l] = acc;
+  }
+  for (int d = 1; d <= 32; d <<= 1) {
+    float q[64];
+    for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ d];
+    memcpy(p, q, sizeof(p));
+  }
+  return p[0];
+}
+
+/* Elementwise fmaf, exported so the numpy oracle's float32 FMA can be
+ * checked against the C library's. */
+void orc_fmaf_array(const float* a, const float* b, const float* c, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = fmaf(a[i], b[i], c[i]);
 }
 
 /* Group-affine row dot: sum_g ( s_g * sum_{k in g} q_k v_k + b_g * vsum_g ). */
@@ -417,8 +467,9 @@ void orc_route_token(const orc_layer* L, const uint16_t* x, int32_t* idx,
   const int E = L->experts, K = L->top_k;
   float logit[1024];
   for (int e = 0; e < E; ++e)
-    logit[e] = round_bf16(orc_router_dot(x, L->router_w + (size_t)e * L->hidden,
-                                         L->hidden));
+    logit[e] = round_bf16(L->router_w ? orc_router_dot(x, L->router_w + (size_t)e * L->hidden,
+                                                       L->hidden)
+                                      : orc_qrouter_dot(&L->router_q, e, x));
   if (logits_out) memcpy(logits_out, logit, (size_t)E * sizeof(float));
   unsigned char taken[1024];
   memset(taken, 0, sizeof(taken));
@@ -455,6 +506,9 @@ int orc_moe_block(const orc_layer* L, const uint16_t* x, int T,
                   float* scores_out, int nthreads) {
   if (!L || !x || !out || T < 0) return ORC_EINVAL;
   if (L->top_k > 64 || L->experts > 1024 || L->top_k > L->experts) return ORC_EINVAL;
+  if (!L->router_w && (!L->router_q.w || L->router_q.rows != L->experts ||
+                       L->router_q.cols != L->hidden || L->router_q.group != 64))
+    return ORC_EINVAL;
   const int H = L->hidden, I = L->inter, K = L->top_k;
   const int has_shared = L->shared_gate_up.w != NULL;
   const int Is = has_shared ? L->shared_inter : 0;
@@ -473,10 +527,11 @@ int orc_moe_block(const orc_layer* L, const uint16_t* x, int T,
     if (scores_out) memcpy(scores_out + (size_t)t * K, scores, (size_t)K * sizeof(float));
     float sgate = 0.0f;
     if (has_shared) {
-      const float sl = L->shared_gate_w
-                           ? round_bf16(orc_router_dot(xt, L->shared_gate_w, H))
-                           : 0.0f;
-      sgate = L->shared_gate_w ? round_bf16(1.0f / (1.0f + expf(-sl))) : 1.0f;
+      const int gated = L->shared_gate_w != NULL || L->shared_gate_q.w != NULL;
+      const float sl = L->shared_gate_w ? round_bf16(orc_router_dot(xt, L->shared_gate_w, H))
+                       : L->shared_gate_q.w ? round_bf16(orc_qrouter_dot(&L->shared_gate_q, 0, xt))
+                                            : 0.0f;
+      sgate = gated ? round_bf16(1.0f / (1.0f + expf(-sl))) : 1.0f;
     }
     float* xv = (float*)malloc((size_t)H * sizeof(float));
     float* xsum = (float*)malloc((size_t)H * sizeof(float));

@@ -36,14 +36,25 @@ def bank_to_dev(q, device="cuda", squeeze=False):
     return (w, s, b)
 
 
+def gate_to_dev(g, device="cuda"):
+    """A bf16 gate (bits) -> bf16 tensor; a quantized one (QWeight [1, rows,
+    H]) -> its (weight, scales, biases) device triple without the expert
+    axis."""
+    from oracle.moe_ref import QWeight
+    if isinstance(g, QWeight):
+        return bank_to_dev(g, device, squeeze=True)
+    return dev_bf16(g, device)
+
+
 def layer_to_dev(L, device="cuda"):
     """oracle.moe_ref.Layer -> runnel_amd.native.LayerHandle (+ tensors)."""
     from runnel_amd import native
     shared = L.shared_gate_up is not None
     return native.make_layer(
-        dev_bf16(L.router_w, device), bank_to_dev(L.gate_up, device),
+        gate_to_dev(L.router_w, device), bank_to_dev(L.gate_up, device),
         bank_to_dev(L.down, device), L.top_k, L.norm_topk_prob,
-        dev_bf16(L.shared_gate_w, device) if shared else None,
+        gate_to_dev(L.shared_gate_w, device) if shared and L.shared_gate_w is not None
+        else None,
         bank_to_dev(L.shared_gate_up, device, squeeze=True) if shared else None,
         bank_to_dev(L.shared_down, device, squeeze=True) if shared else None,
         bits=L.gate_up.bits)
@@ -63,10 +74,16 @@ def layer_from_dev(lw):
     gu = bank_from_dev(*lw.gate_up, lw.bits)
     dn = bank_from_dev(*lw.down, lw.bits)
     E = gu.w.shape[0]
-    L = Layer(gu.cols, gu.rows // 2, E, lw.top_k, host_bf16(lw.router_w), gu, dn,
+
+    def gate(g):
+        if isinstance(g, tuple):
+            return bank_from_dev(*g, 8)
+        return host_bf16(g)
+
+    L = Layer(gu.cols, gu.rows // 2, E, lw.top_k, gate(lw.router_w), gu, dn,
               norm_topk_prob=lw.norm_topk_prob)
     if lw.shared_gate_up is not None:
-        L.shared_gate_w = host_bf16(lw.shared_gate_w)
+        L.shared_gate_w = gate(lw.shared_gate_w)
         L.shared_gate_up = bank_from_dev(*lw.shared_gate_up, lw.bits)
         L.shared_down = bank_from_dev(*lw.shared_down, lw.bits)
     return L

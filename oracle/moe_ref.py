@@ -34,6 +34,18 @@ exact bf16 rounding points inside ``gather_qmm`` and the tie order of
   (bf16 logit descending, expert index ascending).  Because softmax and bf16
   rounding are monotone, that selection is always one valid top-k of
   mlx-lm's bf16 probabilities.
+* A quantized gate (8-bit group-64 ``QuantizedLinear``, the format real
+  checkpoints give ``mlp.gate`` / ``mlp.shared_expert_gate``,
+  bench/runnel_bench/checkpoint.py:200-208) has its own fixed order
+  (``qrouter_logits``: 16-code chunks per lane, per chunk
+  ``fma(sum q x, s, acc)`` then ``fma(sum x, b, acc)``, then the butterfly).
+  Its fp32 FMA is emulated exactly (``fma32``, rounding to odd).  Pinned by
+  the C restatement with libm's fmaf (bit-equal), by a closed form on
+  integer data (every partial sum exact), by the rounding-error bound
+  against the float64 dot, and by constructed double-rounding cases for
+  ``fma32`` itself (tests/test_oracle.py).  mlx's quantized_matmul order is
+  third-party and unpinned; the mlx-lm-style evaluation is held to the
+  north-star tolerance instead.
 * ``block_forward(mode="contract")`` is the HIP kernels' contract: fp32/f64
   arithmetic with bf16 rounding of x_up, x_gate, the SwiGLU activation, each
   expert's down output, the router probabilities/scores, the shared gate and
@@ -208,6 +220,90 @@ def router_logits(x_bits: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
     return p[:, :, 0]
 
 
+def fma32(a, b, c) -> np.ndarray:
+    """Correctly rounded float32 fused multiply-add fl32(a * b + c), the
+    operation of C's fmaf and of the GPU's v_fma_f32.
+
+    a * b is exact in float64 (two 24-bit significands).  The sum is rounded
+    to odd at float64 precision: rounded to nearest, then, when the TwoSum
+    error is nonzero and the result's last bit is even, moved one float64 ulp
+    towards the exact value.  Rounding to odd at 53 bits followed by rounding
+    to nearest at 24 bits equals a single rounding to nearest (Boldo and
+    Melquiond, "Emulation of FMA and correctly rounded sums: proved
+    algorithms using rounding to odd", IEEE Trans. Computers 57(4), 2008;
+    it needs 53 >= 24 + 2)."""
+    a = np.asarray(a, dtype=np.float32).astype(np.float64)
+    b = np.asarray(b, dtype=np.float32).astype(np.float64)
+    c = np.asarray(c, dtype=np.float32).astype(np.float64)
+    p = a * b
+    s = p + c
+    pv = s - c                          # TwoSum: s + err == p + c exactly
+    cv = s - pv
+    err = (c - cv) + (p - pv)
+    even = (np.asarray(s).view(np.int64) & 1) == 0
+    toward = np.where(err > 0, np.inf, -np.inf)
+    s = np.where((err != 0) & even, np.nextafter(s, toward), s)
+    return np.asarray(s).astype(np.float32)
+
+
+def qrouter_logits(x_bits: np.ndarray, qw: "QWeight") -> np.ndarray:
+    """fp32 logits [T, rows] of an MLX-affine quantized gate (the 8-bit
+    group-64 ``QuantizedLinear`` that real checkpoints carry for
+    ``mlp.gate`` and ``mlp.shared_expert_gate``, counted at
+    bench/runnel_bench/checkpoint.py:200-208 and overridden to 8 bits in
+    bench/results/m0/checkpoint-ornith-mlx-8bit.json:163-175), in the GPU
+    router's fixed order.  Not rounded.
+
+    The codes of a row are cut into 16-byte chunks of V = 128 / bits values
+    (a group of 64 spans 64 / V chunks); lane l of 64 takes chunks l, l+64,
+    ... in order, from acc = +0.  For a chunk with inputs x_i, codes q_i and
+    its group's scale s and bias b:
+
+        qa  = q_0 x_0 + q_1 x_1 + ...   sequentially from +0 (products exact)
+        xs  = x_0 + x_1 + ...           sequentially from +0
+        acc = fma(qa, s, acc);  acc = fma(xs, b, acc)
+
+    and the 64 lane sums are combined by the same butterfly as
+    ``router_logits``.  ``qw`` is a one-expert bank [1, rows, H]."""
+    x = bf16_to_f32(x_bits)
+    T, H = x.shape
+    if qw.experts != 1 or qw.cols != H or qw.group != 64:
+        raise ValueError("quantized gate must be a [1, rows, hidden] bank with group 64")
+    V = 128 // qw.bits
+    q = unpack(qw.w[0], qw.bits).astype(np.float32)       # [E, H]
+    s = bf16_to_f32(qw.scales[0])                          # [E, H / 64]
+    b = bf16_to_f32(qw.biases[0])
+    E = q.shape[0]
+    chunks = H // V
+    lanes = np.arange(64)
+    acc = np.zeros((T, E, 64), dtype=np.float32)
+    for i in range((chunks + 63) // 64):
+        c = i * 64 + lanes
+        valid = c < chunks
+        cv = np.where(valid, c, 0)
+        qa = np.zeros((T, E, 64), dtype=np.float32)
+        xs = np.zeros((T, 64), dtype=np.float32)
+        for j in range(V):
+            k = cv * V + j
+            qa = (qa + q[None, :, k] * x[:, None, k]).astype(np.float32)
+            xs = (xs + x[:, k]).astype(np.float32)
+        g = (cv * V) // 64
+        new = fma32(qa, s[None, :, g], acc)
+        new = fma32(np.broadcast_to(xs[:, None, :], new.shape), b[None, :, g], new)
+        acc = np.where(valid[None, None, :], new, acc)
+    for d in (1, 2, 4, 8, 16, 32):
+        acc = (acc + acc[:, :, lanes ^ d]).astype(np.float32)
+    return acc[:, :, 0]
+
+
+def gate_logits(x_bits: np.ndarray, gate) -> np.ndarray:
+    """fp32 router logits [T, rows] for a bf16 gate (bits [rows, H]) or a
+    quantized one (QWeight [1, rows, H])."""
+    if isinstance(gate, QWeight):
+        return qrouter_logits(x_bits, gate)
+    return router_logits(x_bits, gate)
+
+
 def topk_rank(logits_bf16: np.ndarray, k: int) -> np.ndarray:
     """Indices [T, k] ordered by (logit desc, index asc)."""
     order = np.argsort(-logits_bf16, axis=-1, kind="stable")
@@ -234,8 +330,10 @@ def _silu32(v):
 
 
 def route(x_bits, router_w_bits, top_k, norm_topk_prob=True):
-    """-> (idx [T,k] int32, scores [T,k] float32, logits bf16-valued [T,E])."""
-    logits = round_bf16(router_logits(x_bits, router_w_bits))
+    """-> (idx [T,k] int32, scores [T,k] float32, logits bf16-valued [T,E]).
+    ``router_w_bits`` is a bf16 gate [E, H] or a quantized one (QWeight
+    [1, E, H])."""
+    logits = round_bf16(gate_logits(x_bits, router_w_bits))
     idx = topk_rank(logits, top_k)
     m = logits.max(axis=-1, keepdims=True)
     e = np.exp((logits - m).astype(np.float32)).astype(np.float32)
@@ -388,7 +486,9 @@ def block_forward(layer: Layer, x_bits: np.ndarray, residual_bits=None,
         xf = bf16_to_f32(x_bits)
         ysh = expert_ffn(layer.shared_gate_up, layer.shared_down, 0, xf, mode)
         if layer.shared_gate_w is not None:
-            sl = round_bf16(router_logits(x_bits, layer.shared_gate_w[None, :])[:, 0])
+            sgw = layer.shared_gate_w
+            sl = round_bf16(gate_logits(x_bits, sgw if isinstance(sgw, QWeight)
+                                        else sgw[None, :])[:, 0])
             sg = round_bf16(_sigmoid32(sl))[:, None]
         else:
             sg = np.ones((T, 1), dtype=np.float32)
@@ -420,9 +520,10 @@ def gather_sort(indices: np.ndarray):
 
 def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8,
                bits=8, group=64, shared=True, w_std=0.02, router_std=0.02,
-               shared_inter=None) -> Layer:
+               shared_inter=None, router_bits=None) -> Layer:
     """Weights ~ N(0, w_std) quantized with ``quantize``; router and shared
-    gate ~ N(0, router_std) in bf16."""
+    gate ~ N(0, router_std) in bf16, or quantized to ``router_bits`` (one-
+    expert banks [1, E, H] and [1, 1, H]) when it is given."""
     rng = np.random.default_rng(seed)
     shared_inter = inter if shared_inter is None else shared_inter
 
@@ -432,14 +533,19 @@ def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8,
         return QWeight(words.reshape(e, rows, -1), s.reshape(e, rows, -1),
                        b.reshape(e, rows, -1), bits, group)
 
-    router = f32_to_bf16(rng.standard_normal((experts, hidden), dtype=np.float32)
-                         * np.float32(router_std))
+    def gate(rows):
+        w = rng.standard_normal((rows, hidden), dtype=np.float32) * np.float32(router_std)
+        if router_bits is None:
+            return f32_to_bf16(w if rows > 1 else w[0])
+        words, s, b = quantize(w, router_bits, group)
+        return QWeight(words[None], s[None], b[None], router_bits, group)
+
+    router = gate(experts)
     gu = qbank(experts, 2 * inter, hidden)
     dn = qbank(experts, hidden, inter)
     layer = Layer(hidden, inter, experts, top_k, router, gu, dn)
     if shared:
-        layer.shared_gate_w = f32_to_bf16(
-            rng.standard_normal(hidden, dtype=np.float32) * np.float32(router_std))
+        layer.shared_gate_w = gate(1)
         layer.shared_gate_up = qbank(1, 2 * shared_inter, hidden)
         layer.shared_down = qbank(1, hidden, shared_inter)
     return layer
@@ -475,6 +581,9 @@ def c_oracle():
     lib.orc_qmm_build.argtypes = [ctypes.c_int, S, S, S, P, P, P, P, P]
     lib.orc_router_dot.argtypes = [P, P, ctypes.c_int]
     lib.orc_router_dot.restype = ctypes.c_float
+    lib.orc_qrouter_dot.argtypes = [P, ctypes.c_int, P]
+    lib.orc_qrouter_dot.restype = ctypes.c_float
+    lib.orc_fmaf_array.argtypes = [P, P, P, P, S]
     lib.orc_moe_block.argtypes = [P, P, ctypes.c_int, P, P, P, P, ctypes.c_int]
     lib.orc_random_sequence.argtypes = [ctypes.c_uint64, S, P]
     lib.orc_random_sequence.restype = ctypes.c_uint32
@@ -598,7 +707,7 @@ class _CLayer(ctypes.Structure):
                 ("top_k", ctypes.c_int32), ("norm_topk_prob", ctypes.c_int32),
                 ("router_w", ctypes.c_void_p), ("shared_gate_w", ctypes.c_void_p),
                 ("gate_up", _CQW), ("down", _CQW), ("shared_gate_up", _CQW),
-                ("shared_down", _CQW)]
+                ("shared_down", _CQW), ("router_q", _CQW), ("shared_gate_q", _CQW)]
 
 
 def _cqw(q: QWeight | None, keep):
@@ -616,14 +725,19 @@ def c_block_forward(layer: Layer, x_bits: np.ndarray, residual_bits=None,
     """The same block contract through oracle/cpu_moe.c (fp32, OpenMP)."""
     lib = c_oracle()
     keep: list = []
-    router = np.ascontiguousarray(layer.router_w)
-    sg = None if layer.shared_gate_w is None else np.ascontiguousarray(layer.shared_gate_w)
+    rq = layer.router_w if isinstance(layer.router_w, QWeight) else None
+    sgq = layer.shared_gate_w if isinstance(layer.shared_gate_w, QWeight) else None
+    router = None if rq is not None else np.ascontiguousarray(layer.router_w)
+    sg = (None if layer.shared_gate_w is None or sgq is not None
+          else np.ascontiguousarray(layer.shared_gate_w))
     keep += [router, sg]
     cl = _CLayer(layer.hidden, layer.inter, layer.shared_inter, layer.experts,
-                 layer.top_k, int(layer.norm_topk_prob), _p(router).value,
+                 layer.top_k, int(layer.norm_topk_prob),
+                 None if router is None else _p(router).value,
                  None if sg is None else _p(sg).value,
                  _cqw(layer.gate_up, keep), _cqw(layer.down, keep),
-                 _cqw(layer.shared_gate_up, keep), _cqw(layer.shared_down, keep))
+                 _cqw(layer.shared_gate_up, keep), _cqw(layer.shared_down, keep),
+                 _cqw(rq, keep), _cqw(sgq, keep))
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     T = x.shape[0]
     out = np.zeros((T, layer.hidden), np.uint16)

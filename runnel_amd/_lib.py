@@ -21,7 +21,7 @@ RMOE_EWS = -4
 RMOE_EHIP = -5
 RMOE_ENULL = -6
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EXPORTED = (
     "rmoe_abi_version", "rmoe_last_error", "rmoe_status_string",
@@ -29,7 +29,7 @@ EXPORTED = (
     "rmoe_switch_glu", "rmoe_switch_workspace_bytes", "rmoe_gather_qmm",
     "rmoe_moe_block", "rmoe_quantize", "rmoe_dequantize", "rmoe_stream_read",
     "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes", "rmoe_chain_table_pack",
-    "rmoe_moe_chain", "rmoe_workspace_status_offset",
+    "rmoe_moe_chain", "rmoe_workspace_status_offset", "rmoe_router_q",
 )
 
 
@@ -60,6 +60,7 @@ class Layer(ctypes.Structure):
         ("router_w", ctypes.c_void_p), ("shared_gate_w", ctypes.c_void_p),
         ("gate_up", QWeight), ("down", QWeight),
         ("shared_gate_up", QWeight), ("shared_down", QWeight),
+        ("router_q", QWeight), ("shared_gate_q", QWeight),
     ]
 
 
@@ -98,6 +99,7 @@ def load() -> ctypes.CDLL:
         lib.rmoe_switch_workspace_bytes.restype = SZ
         lib.rmoe_switch_workspace_bytes.argtypes = [QP, QP, I32, I32]
         lib.rmoe_router.argtypes = [P, I32, I32, I32, I32, P, I32, P, P, P, SZ, P]
+        lib.rmoe_router_q.argtypes = [QP, I32, I32, P, I32, P, P, P, SZ, P]
         lib.rmoe_router_workspace_bytes.restype = SZ
         lib.rmoe_router_workspace_bytes.argtypes = [I32, I32, I32]
         lib.rmoe_switch_glu.argtypes = [QP, QP, P, I32, P, I32, P, P, SZ, P]

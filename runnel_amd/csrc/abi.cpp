@@ -64,6 +64,19 @@ int check_qweight(const rmoe_qweight* q, const char* name) {
   return RMOE_OK;
 }
 
+// A quantized gate: one 8-bit group-64 bank [1, rows, hidden] (the format of
+// the checkpoints' mlp.gate / mlp.shared_expert_gate).
+int check_gate_q(const rmoe_qweight* q, int rows, int hidden, const char* name) {
+  int rc;
+  if ((rc = check_qweight(q, name))) return rc;
+  if (q->bits != 8)
+    return fail(RMOE_EBITS, "%s: quantized gates must be 8-bit (got %d)", name, q->bits);
+  if (q->experts != 1 || q->rows != rows || q->cols != hidden)
+    return fail(RMOE_EINVAL, "%s must be [1, %d, %d] (got [%d, %d, %d])", name, rows, hidden,
+                q->experts, q->rows, q->cols);
+  return RMOE_OK;
+}
+
 // The down-projection kernel maps one row onto inter/values_per_chunk lanes.
 int check_down_width(int inter, int bits, const char* name) {
   const int chunks = inter / values_per_chunk(bits);
@@ -89,10 +102,16 @@ int check_layer(const rmoe_layer* L) {
   if (L->top_k < 1 || L->top_k > rmoe::kMaxTopK || L->top_k > L->experts)
     return fail(RMOE_EINVAL, "top_k must be in [1, min(%d, experts)] (got %d)",
                 rmoe::kMaxTopK, L->top_k);
-  if (!L->router_w) return fail(RMOE_ENULL, "router_w is NULL");
-  if (!aligned(L->router_w, 16))
-    return fail(RMOE_EALIGN, "router_w must be 16-byte aligned");
   int rc;
+  const bool rq = L->router_q.w != nullptr;
+  if (rq == (L->router_w != nullptr))
+    return fail(rq ? RMOE_EINVAL : RMOE_ENULL,
+                "exactly one of router_w (bf16) and router_q (8-bit) must be given");
+  if (rq) {
+    if ((rc = check_gate_q(&L->router_q, L->experts, L->hidden, "router_q"))) return rc;
+  } else if (!aligned(L->router_w, 16)) {
+    return fail(RMOE_EALIGN, "router_w must be 16-byte aligned");
+  }
   if ((rc = check_qweight(&L->gate_up, "gate_up"))) return rc;
   if ((rc = check_qweight(&L->down, "down"))) return rc;
   if (L->gate_up.experts != L->experts || L->gate_up.rows != 2 * L->inter ||
@@ -122,12 +141,25 @@ int check_layer(const rmoe_layer* L) {
     if (L->shared_gate_up.bits != L->gate_up.bits ||
         L->shared_down.bits != L->gate_up.bits)
       return fail(RMOE_EBITS, "shared expert must use the routed bit width");
-  } else if (L->shared_gate_w) {
-    return fail(RMOE_EINVAL, "shared_gate_w given without a shared expert");
+  } else if (L->shared_gate_w || L->shared_gate_q.w) {
+    return fail(RMOE_EINVAL, "shared gate given without a shared expert");
   }
+  if (L->shared_gate_w && L->shared_gate_q.w)
+    return fail(RMOE_EINVAL, "give at most one of shared_gate_w and shared_gate_q");
+  if ((rq && L->shared_gate_w) || (!rq && L->shared_gate_q.w))
+    return fail(RMOE_EINVAL,
+                "the shared gate must use the router's format (both bf16 or both 8-bit)");
+  if (L->shared_gate_q.w &&
+      (rc = check_gate_q(&L->shared_gate_q, 1, L->hidden, "shared_gate_q")))
+    return rc;
   if (L->shared_gate_w && !aligned(L->shared_gate_w, 16))
     return fail(RMOE_EALIGN, "shared_gate_w must be 16-byte aligned");
   return RMOE_OK;
+}
+
+bool router_quantized(const rmoe_layer* L) { return L->router_q.w != nullptr; }
+bool shared_gated(const rmoe_layer* L) {
+  return L->shared_gate_up.w != nullptr && (L->shared_gate_w || L->shared_gate_q.w);
 }
 
 size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
@@ -137,6 +169,7 @@ struct Layout {
   size_t ctr, fused, logits, idx, scores, act, total;
   // expert-sorted (prefill) path
   size_t rows, offs, tile_offs, tile_desc, hist, act16, y16, wnorm;
+  size_t split;  // bf16 planes of a quantized gate (matrix-core router)
 };
 
 // Calls that route at least kPrefillMinRows (token, slot) rows take the
@@ -152,7 +185,7 @@ bool prefill_path(int T, int K, int E, int H, int I) {
 // finds them at zero (every kernel leaves them at zero when it finishes).
 // The router's logits / indices / scores come next in both paths.
 Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
-              bool combine = false) {
+              bool combine = false, bool split = false) {
   Layout l{};
   size_t off = 0;
   l.ctr = off;
@@ -182,6 +215,10 @@ Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
     off = align_up(off + (size_t)rmoe::prefill_sort_slices(T, K) * (E + 2) * sizeof(int32_t));
     l.wnorm = off;
     off = align_up(off + (size_t)E * sizeof(float));
+    if (split) {
+      l.split = off;
+      off = align_up(off + 2 * (size_t)E * H * sizeof(uint16_t));
+    }
     l.act16 = off;
     off = align_up(off + R * I * sizeof(uint16_t));
     if (combine) {
@@ -195,7 +232,9 @@ Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
 
 Layout block_layout(const rmoe_layer* L, int T) {
   const bool sorted = prefill_path(T, L->top_k, L->experts, L->hidden, L->inter);
-  return layout(T, L->experts, L->top_k, L->inter, L->hidden, sorted, true);
+  const bool split = sorted && router_quantized(L) &&
+                     rmoe::router_mfma_eligible(L->experts, L->hidden);
+  return layout(T, L->experts, L->top_k, L->inter, L->hidden, sorted, true, split);
 }
 
 rmoe::PrefillArgs prefill_args(const Layout& l, void* ws, int T, int H, int I, int E, int K,
@@ -252,8 +291,12 @@ rmoe::DecodeArgs decode_args(const rmoe_layer* L, const uint16_t* x, int T,
   a.norm = L->norm_topk_prob != 0;
   a.switch_mode = 0;
   a.x = x;
+  a.rq8 = router_quantized(L);
+  a.has_sg = shared_gated(L);
   a.router_w = L->router_w;
   a.sgate_w = a.has_shared ? L->shared_gate_w : nullptr;
+  a.rq = qw(L->router_q);
+  a.sgq = qw(L->shared_gate_q);
   a.gu = qw(L->gate_up);
   a.dn = qw(L->down);
   a.sgu = qw(L->shared_gate_up);
@@ -274,7 +317,7 @@ bool fused_eligible(const rmoe_layer* L, int* grid) {
   if (L->hidden != rmoe::kFusedH || L->inter != rmoe::kFusedI) return false;
   if (units > rmoe::kMaxFusedUnits || L->experts > rmoe::kFusedMaxExperts) return false;
   int g = 0;
-  if (rmoe::fused_grid(L->gate_up.bits, &g) != hipSuccess) return false;
+  if (rmoe::fused_grid(L->gate_up.bits, router_quantized(L), &g) != hipSuccess) return false;
   const int waves = g * (rmoe::kFusedThreads / 64);
   // the router rows are computed once per XCD by its g / 8 workgroups
   if (g % 8 != 0 || g < L->experts) return false;
@@ -295,6 +338,8 @@ rmoe::FusedLayer fused_layer(const rmoe_layer* L) {
   f.dn = qw(L->down);
   f.sgu = qw(L->shared_gate_up);
   f.sdn = qw(L->shared_down);
+  f.rq = qw(L->router_q);
+  f.sgq = qw(L->shared_gate_q);
   return f;
 }
 
@@ -306,6 +351,7 @@ rmoe::FusedArgs fused_args(const rmoe_layer* L, const uint16_t* x, uint16_t* out
   f.K = L->top_k;
   f.norm = L->norm_topk_prob != 0;
   f.has_shared = L->shared_gate_up.w != nullptr;
+  f.rq8 = router_quantized(L);
   f.layer0 = fused_layer(L);
   f.table = nullptr;
   f.x = x;
@@ -396,6 +442,40 @@ int rmoe_router(const uint16_t* router_w, int32_t experts, int32_t hidden,
   return ok();
 }
 
+int rmoe_router_q(const rmoe_qweight* router, int32_t top_k, int32_t norm_topk_prob,
+                  const uint16_t* x, int32_t tokens, int32_t* indices, float* scores,
+                  void* ws, size_t ws_bytes, void* stream) {
+  int rc;
+  if (!router) return fail(RMOE_ENULL, "router is NULL");
+  const int experts = router->rows;
+  const int hidden = router->cols;
+  if ((rc = check_gate_q(router, experts, hidden, "router"))) return rc;
+  if (experts > rmoe::kMaxExperts)
+    return fail(RMOE_EINVAL, "experts must be in [1, %d] (got %d)", rmoe::kMaxExperts,
+                experts);
+  if (top_k < 1 || top_k > rmoe::kMaxTopK || top_k > experts)
+    return fail(RMOE_EINVAL, "top_k must be in [1, min(%d, experts)] (got %d)",
+                rmoe::kMaxTopK, top_k);
+  if ((rc = check_tokens(tokens))) return rc;
+  if (tokens == 0) return ok();
+  if (!x || !indices || !scores) return fail(RMOE_ENULL, "x, indices and scores are required");
+  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  const size_t need = layout(tokens, experts, top_k, 0).total;
+  if ((rc = check_ws(ws, ws_bytes, need))) return rc;
+  rmoe_layer L{};
+  L.hidden = hidden;
+  L.experts = experts;
+  L.top_k = top_k;
+  L.norm_topk_prob = norm_topk_prob;
+  L.router_q = *router;
+  rmoe::DecodeArgs a = decode_args(&L, x, tokens, ws);
+  a.idx_out = indices;
+  a.scores_out = scores;
+  const hipError_t e = rmoe::launch_router(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  return ok();
+}
+
 int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
                    const uint16_t* residual, uint16_t* out, int32_t* indices_out,
                    float* scores_out, void* ws, size_t ws_bytes, void* stream) {
@@ -433,7 +513,9 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   hipError_t e;
   if (lay.rows && rmoe::router_mfma_eligible(L->experts, L->hidden))
     e = rmoe::launch_router_mfma(
-        a, reinterpret_cast<float*>(static_cast<char*>(ws) + lay.wnorm), s);
+        a, reinterpret_cast<float*>(static_cast<char*>(ws) + lay.wnorm),
+        lay.split ? reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + lay.split) : nullptr,
+        s);
   else
     e = rmoe::launch_router(a, s);
   if (e != hipSuccess) return hip_fail(e, "router launch");
@@ -598,8 +680,13 @@ int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers, void* host
         b.top_k != a.top_k || b.norm_topk_prob != a.norm_topk_prob ||
         b.gate_up.bits != a.gate_up.bits ||
         (b.shared_gate_up.w == nullptr) != (a.shared_gate_up.w == nullptr) ||
-        (b.shared_gate_w == nullptr) != (a.shared_gate_w == nullptr))
+        (b.shared_gate_w == nullptr) != (a.shared_gate_w == nullptr) ||
+        (b.router_q.w == nullptr) != (a.router_q.w == nullptr) ||
+        (b.shared_gate_q.w == nullptr) != (a.shared_gate_q.w == nullptr))
       return fail(RMOE_EINVAL, "layer %d differs in shape or format from layer 0", i);
+  }
+  for (int i = 0; i < n_layers; ++i) {
+    const rmoe_layer& b = layers[i];
     if (!fused_eligible(&b, &grid))
       return fail(RMOE_EINVAL,
                   "chained decode needs hidden %d, inter %d, top_k + shared <= %d, "

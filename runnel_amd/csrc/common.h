@@ -180,6 +180,21 @@ __device__ __forceinline__ float qdot_chunk(const uint4 w, const float* v) {
   return acc;
 }
 
+// One 16-byte chunk (16 codes) of an 8-bit MLX-affine gate row folded into
+// a router lane's partial, in the fixed order of the quantized router
+// contract: qa = sum q_i v_i and xs = sum v_i, each sequential from +0 (the
+// products are exact), then acc = fma(qa, s, acc), acc = fma(xs, b, acc)
+// with the chunk's group scale and bias.
+__device__ __forceinline__ float qgate_chunk(float acc, const uint4 w, const float* v, float s,
+                                             float b) {
+  const float qa = qdot_chunk<8>(w, v);
+  float xs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xs += v[i];
+  acc = fmaf(qa, s, acc);
+  return fmaf(xs, b, acc);
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint4 load16(const void* p) {

@@ -55,9 +55,91 @@ __device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const f
   }
   if (lane == 0) {
     float sg = 1.0f;
-    if (p.sgate_w) sg = round_bf16(sigmoid(round_bf16(sg_logit)));
+    if (p.has_sg) sg = round_bf16(sigmoid(round_bf16(sg_logit)));
     p.scores[t * (p.K + 1) + p.K] = sg;
   }
+}
+
+// One lane's partial of a bf16 gate row (the router contract): chunks
+// lane + 64 i of 8 values, element by element.  All loads of a batch are
+// issued before the first multiply (one memory round trip per batch).
+__device__ __forceinline__ float bf16_gate_partial(const uint16_t* wr, const uint16_t* xt, int H,
+                                                   int lane) {
+  float acc = 0.0f;
+  const int chunks = H >> 3;
+  for (int c0 = lane; c0 < chunks; c0 += 64 * kRouterBatch) {
+    uint4 xv[kRouterBatch], wv[kRouterBatch];
+#pragma unroll
+    for (int i = 0; i < kRouterBatch; ++i) {
+      const int c = c0 + 64 * i;
+      xv[i] = wv[i] = make_uint4(0, 0, 0, 0);
+      if (c < chunks) {
+        xv[i] = load16(xt + c * 8);
+        wv[i] = load16_stream(wr + c * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRouterBatch; ++i) {
+      if (c0 + 64 * i < chunks) {
+        acc = fmaf(bf16_lo(xv[i].x), bf16_lo(wv[i].x), acc);
+        acc = fmaf(bf16_hi(xv[i].x), bf16_hi(wv[i].x), acc);
+        acc = fmaf(bf16_lo(xv[i].y), bf16_lo(wv[i].y), acc);
+        acc = fmaf(bf16_hi(xv[i].y), bf16_hi(wv[i].y), acc);
+        acc = fmaf(bf16_lo(xv[i].z), bf16_lo(wv[i].z), acc);
+        acc = fmaf(bf16_hi(xv[i].z), bf16_hi(wv[i].z), acc);
+        acc = fmaf(bf16_lo(xv[i].w), bf16_lo(wv[i].w), acc);
+        acc = fmaf(bf16_hi(xv[i].w), bf16_hi(wv[i].w), acc);
+      }
+    }
+  }
+  return acc;
+}
+
+// 16 bf16 inputs (two 16-byte pieces) as floats.
+__device__ __forceinline__ void unpack_x16(const uint4 a, const uint4 b, float (&v)[16]) {
+  const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[2 * i] = bf16_lo(u[i]);
+    v[2 * i + 1] = bf16_hi(u[i]);
+  }
+}
+
+// One lane's partial of row `row` of an 8-bit MLX-affine gate bank (the
+// quantized router contract): chunks lane + 64 i of 16 codes.
+__device__ __forceinline__ float q8_gate_partial(const QW& bank, size_t row, const uint16_t* xt,
+                                                 int H, int lane) {
+  const int chunks = H >> 4;
+  const uint32_t* wr = bank.w + row * (size_t)(H >> 2);
+  const uint16_t* sr = bank.s + row * (size_t)(H >> 6);
+  const uint16_t* br = bank.b + row * (size_t)(H >> 6);
+  float acc = 0.0f;
+  for (int c0 = lane; c0 < chunks; c0 += 64 * kRouterBatch) {
+    uint4 wv[kRouterBatch], xa[kRouterBatch], xb[kRouterBatch];
+    uint32_t sv[kRouterBatch], bv[kRouterBatch];
+#pragma unroll
+    for (int i = 0; i < kRouterBatch; ++i) {
+      const int c = c0 + 64 * i;
+      wv[i] = xa[i] = xb[i] = make_uint4(0, 0, 0, 0);
+      sv[i] = bv[i] = 0;
+      if (c < chunks) {
+        wv[i] = load16_stream(wr + c * 4);
+        xa[i] = load16(xt + c * 16);
+        xb[i] = load16(xt + c * 16 + 8);
+        sv[i] = sr[c >> 2];
+        bv[i] = br[c >> 2];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRouterBatch; ++i) {
+      if (c0 + 64 * i < chunks) {
+        float v[16];
+        unpack_x16(xa[i], xb[i], v);
+        acc = qgate_chunk(acc, wv[i], v, bf16_to_f32(sv[i]), bf16_to_f32(bv[i]));
+      }
+    }
+  }
+  return acc;
 }
 
 template <int P>
@@ -65,43 +147,19 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   const int t = blockIdx.y;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int has_sg = p.sgate_w != nullptr;
+  const int has_sg = p.has_sg;
   const int R = p.E + has_sg;
   const int row = blockIdx.x * 4 + wave;
   const uint16_t* xt = p.x + (size_t)t * p.H;
   float* lg = p.logits + (size_t)t * (p.E + 1);
   if (row < R) {
-    const uint16_t* wr =
-        row < p.E ? p.router_w + (size_t)row * p.H : p.sgate_w;
-    float acc = 0.0f;
-    const int chunks = p.H >> 3;
-    // All loads of the row are issued before the first multiply (one memory
-    // round trip); the accumulation order is still chunk by chunk.
-    for (int c0 = lane; c0 < chunks; c0 += 64 * kRouterBatch) {
-      uint4 xv[kRouterBatch], wv[kRouterBatch];
-#pragma unroll
-      for (int i = 0; i < kRouterBatch; ++i) {
-        const int c = c0 + 64 * i;
-        xv[i] = wv[i] = make_uint4(0, 0, 0, 0);
-        if (c < chunks) {
-          xv[i] = load16(xt + c * 8);
-          wv[i] = load16_stream(wr + c * 8);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kRouterBatch; ++i) {
-        if (c0 + 64 * i < chunks) {
-          acc = fmaf(bf16_lo(xv[i].x), bf16_lo(wv[i].x), acc);
-          acc = fmaf(bf16_hi(xv[i].x), bf16_hi(wv[i].x), acc);
-          acc = fmaf(bf16_lo(xv[i].y), bf16_lo(wv[i].y), acc);
-          acc = fmaf(bf16_hi(xv[i].y), bf16_hi(wv[i].y), acc);
-          acc = fmaf(bf16_lo(xv[i].z), bf16_lo(wv[i].z), acc);
-          acc = fmaf(bf16_hi(xv[i].z), bf16_hi(wv[i].z), acc);
-          acc = fmaf(bf16_lo(xv[i].w), bf16_lo(wv[i].w), acc);
-          acc = fmaf(bf16_hi(xv[i].w), bf16_hi(wv[i].w), acc);
-        }
-      }
-    }
+    float acc;
+    if (p.rq8)
+      acc = q8_gate_partial(row < p.E ? p.rq : p.sgq, row < p.E ? (size_t)row : 0, xt, p.H,
+                            lane);
+    else
+      acc = bf16_gate_partial(row < p.E ? p.router_w + (size_t)row * p.H : p.sgate_w, xt, p.H,
+                              lane);
     acc = wave_sum(acc);
     if (lane == 0) store_coherent(lg + row, acc);
   }
@@ -133,13 +191,21 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
 // ------------------------------------------------ prefill router (MFMA)
 // For many tokens the router is a [T, H] x [H, E] product.  The logits are
 // computed on the matrix cores in fp32 (order of the hardware's choosing),
-// then every token's selection is settled exactly:
+// then every token's selection is settled exactly.  For a bf16 gate:
 //
 //   |L - exact| <= (H - 1) 2^-23 S   any order of fp32 sums of the exact
 //                                    bf16 products (round to nearest or
 //                                    toward zero)
 //   |c - exact| <= (H/64 + 8) 2^-24 S  the router contract's order
 //   S = sum |x_k w_k| <= |x|_2 max_e |w_e|_2
+//
+// An 8-bit gate is first split into two bf16 planes, hi = bf16(w) and
+// lo = bf16(w - hi) with w = fl32(q s + b), so |w - hi - lo| <= 2^-18 |w|;
+// L sums the 2H products of x with both planes, and with
+// S = sum |x_k| (|q_k s| + |b|) <= |x|_2 max_e || |q s| + |b| ||_2:
+//
+//   |L - exact| <= ((2H - 1) 2^-23 (1 + 2^-7) + 2^-17) S
+//   |c - exact| <= (15 + 2 ceil(H / 1024) + 8) 2^-24 S   (quantized contract)
 //
 // so with delta the sum of both bounds (plus a denormal allowance), an
 // expert whose L is more than margin = 2 delta + one bf16 ulp (at the
@@ -169,12 +235,60 @@ __global__ __launch_bounds__(256) void router_rownorm_kernel(const DecodeArgs p,
   if (lane == 0) wnorm[e] = sqrtf(s) * (1.0f + 1.0f / 1024.0f);
 }
 
+// 8-bit gate rows as two bf16 planes hi = bf16(w), lo = bf16(w - hi) of
+// w = fl32(q s + b) (w - hi is exact), and the row bound
+// || |q s| + |b| ||_2.  One wave per row, 16 codes per lane and step.
+__global__ __launch_bounds__(256) void router_split_kernel(const DecodeArgs p, uint16_t* hi,
+                                                           uint16_t* lo, float* wnorm) {
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (e >= p.E) return;
+  const int H = p.H;
+  const uint32_t* wr = p.rq.w + (size_t)e * (H >> 2);
+  const uint16_t* sr = p.rq.s + (size_t)e * (H >> 6);
+  const uint16_t* br = p.rq.b + (size_t)e * (H >> 6);
+  uint16_t* hr = hi + (size_t)e * H;
+  uint16_t* lr = lo + (size_t)e * H;
+  float n2 = 0.0f;
+  for (int c = lane; c < (H >> 4); c += 64) {
+    const uint4 w = load16(wr + c * 4);
+    const float sc = bf16_to_f32(sr[c >> 2]);
+    const float bi = bf16_to_f32(br[c >> 2]);
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    uint32_t ph[8], pl[8];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float q = (float)((words[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+      const float v = fmaf(q, sc, bi);                 // q s exact: one rounding
+      const uint32_t h = f32_to_bf16(v);
+      const uint32_t l = f32_to_bf16(v - bf16_to_f32(h));
+      const float m = fabsf(q * sc) + fabsf(bi);
+      n2 = fmaf(m, m, n2);
+      if (j & 1) {
+        ph[j >> 1] |= h << 16;
+        pl[j >> 1] |= l << 16;
+      } else {
+        ph[j >> 1] = h;
+        pl[j >> 1] = l;
+      }
+    }
+    *reinterpret_cast<uint4*>(hr + c * 16) = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    *reinterpret_cast<uint4*>(hr + c * 16 + 8) = make_uint4(ph[4], ph[5], ph[6], ph[7]);
+    *reinterpret_cast<uint4*>(lr + c * 16) = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    *reinterpret_cast<uint4*>(lr + c * 16 + 8) = make_uint4(pl[4], pl[5], pl[6], pl[7]);
+  }
+  n2 = wave_sum(n2);
+  if (lane == 0) wnorm[e] = sqrtf(n2) * (1.0f + 1.0f / 1024.0f);
+}
+
 typedef __bf16 bf16x8_r __attribute__((ext_vector_type(8)));
 typedef float f32x4_r __attribute__((ext_vector_type(4)));
 
 // One wave: 16 tokens x 64 experts, K in chunks of 64 (four chunks of
 // loads in flight per lane); lane (col, g) holds A row / B column `col` and
-// k = 16 g + [0, 16) of each chunk.
+// k = 16 g + [0, 16) of each chunk.  ACC: continue the sums already in
+// `logits` (the second plane of a split gate).
+template <bool ACC>
 __global__ __launch_bounds__(64) void router_logits16_kernel(const DecodeArgs p) {
   const int lane = threadIdx.x;
   const int col = lane & 15;
@@ -188,7 +302,16 @@ __global__ __launch_bounds__(64) void router_logits16_kernel(const DecodeArgs p)
   for (int cb = 0; cb < 4; ++cb) wb[cb] = p.router_w + (size_t)(e0 + cb * 16 + col) * p.H + g * 16;
   f32x4_r acc[4];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+  for (int cb = 0; cb < 4; ++cb) {
+    acc[cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+    if constexpr (ACC) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 4 * g + i;
+        if (t < p.T) acc[cb][i] = p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col];
+      }
+    }
+  }
   const int nch = p.H / 64;
   for (int c0 = 0; c0 < nch; c0 += 4) {
     u32x4 a[4][2], b[4][4][2];
@@ -223,6 +346,7 @@ __global__ __launch_bounds__(64) void router_logits16_kernel(const DecodeArgs p)
 // Long prefills: one wave takes 64 tokens x 64 experts (4 x 4 MFMA tiles),
 // so each router row is read once per 64 tokens; K in chunks of 64 with the
 // next chunk's loads in flight, same lane layout.
+template <bool ACC>
 __global__ __launch_bounds__(64) void router_logits64_kernel(const DecodeArgs p) {
   constexpr int kRouterTB = 4;  // 16-token blocks per wave
   const int lane = threadIdx.x;
@@ -241,7 +365,16 @@ __global__ __launch_bounds__(64) void router_logits64_kernel(const DecodeArgs p)
 #pragma unroll
   for (int tb = 0; tb < kRouterTB; ++tb)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < 4; ++cb) {
+      acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+      if constexpr (ACC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = t0 + tb * 16 + 4 * g + i;
+          if (t < p.T) acc[tb][cb][i] = p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col];
+        }
+      }
+    }
   auto load = [&](int c, u32x4 (&a)[kRouterTB][2], u32x4 (&b)[4][2]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -323,7 +456,38 @@ __device__ __forceinline__ float f32_from_order_key(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// One wave per token (E <= 256, H a multiple of 512 up to 4096).
+// The quantized router contract's dot of one token row (held as xv: chunk
+// lane + 64 i in xv[2 i], xv[2 i + 1]) with row `row` of an 8-bit gate bank.
+__device__ __forceinline__ float q8_contract_dot(const uint4 (&xv)[8], const QW& bank, size_t row,
+                                                 int H) {
+  const int lane = threadIdx.x & 63;
+  const int chunks = H >> 4;
+  uint4 wv[4];
+  uint32_t sv[4], bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ch = lane + 64 * i;
+    if (ch < chunks) {
+      wv[i] = load16(bank.w + row * (size_t)(H >> 2) + ch * 4);
+      sv[i] = bank.s[row * (size_t)(H >> 6) + (ch >> 2)];
+      bv[i] = bank.b[row * (size_t)(H >> 6) + (ch >> 2)];
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (lane + 64 * i < chunks) {
+      float v[16];
+      unpack_x16(xv[2 * i], xv[2 * i + 1], v);
+      acc = qgate_chunk(acc, wv[i], v, bf16_to_f32(sv[i]), bf16_to_f32(bv[i]));
+    }
+  }
+  return wave_sum(acc);
+}
+
+// One wave per token (E <= 256, H a multiple of 512 up to 4096).  RQ: the
+// gates are 8-bit banks (the logits came from their split planes).
+template <int RQ>
 __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
                                                             const float* wnorm) {
   constexpr int P = 4;
@@ -335,18 +499,25 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
   if (t >= p.T) return;
   const float* lg = p.logits + (size_t)t * (p.E + 1);
   const int nxc = p.H / 512;
+  const uint16_t* xt = p.x + (size_t)t * p.H;
+  // bf16 contract: 16-byte piece c is chunk lane + 64 c (8 values); quantized
+  // contract: pieces 2 i, 2 i + 1 are chunk lane + 64 i (16 values)
   uint4 xv[XC];
   float nx2 = 0.0f;
 #pragma unroll
   for (int c = 0; c < XC; ++c) {
-    if (c < nxc) {
-      xv[c] = load16(p.x + (size_t)t * p.H + (lane + 64 * c) * 8);
-      const uint32_t vv[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+    xv[c] = make_uint4(0, 0, 0, 0);
+    if constexpr (RQ) {
+      const int ch = lane + 64 * (c >> 1);
+      if (ch < (p.H >> 4)) xv[c] = load16(xt + ch * 16 + (c & 1) * 8);
+    } else {
+      if (c < nxc) xv[c] = load16(xt + (lane + 64 * c) * 8);
+    }
+    const uint32_t vv[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        nx2 = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), nx2);
-        nx2 = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), nx2);
-      }
+    for (int i = 0; i < 4; ++i) {
+      nx2 = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), nx2);
+      nx2 = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), nx2);
     }
   }
   const float nx = sqrtf(wave_sum(nx2)) * (1.0f + 1.0f / 1024.0f);
@@ -376,7 +547,10 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
     if (cnt >= p.K) thr = cand;
   }
   const float tk = f32_from_order_key(thr);
-  const float gam = (float)(p.H - 1) * 0x1p-23f + (float)(p.H / 64 + 8) * 0x1p-24f;
+  const float gam =
+      RQ ? (float)(2 * p.H - 1) * 0x1p-23f * (1.0f + 0x1p-7f) + 0x1p-17f +
+               (float)(15 + 2 * ((p.H + 1023) / 1024) + 8) * 0x1p-24f
+         : (float)(p.H - 1) * 0x1p-23f + (float)(p.H / 64 + 8) * 0x1p-24f;
   const float delta = gam * nx * wn + 0x1p-100f * (1.0f + nx + wn);
   const float mag = amax + 2.0f * delta + 1.0f;
   const int ex = (int)((__float_as_uint(mag) >> 23) & 0xFFu);
@@ -393,12 +567,14 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
       const int bit = __ffsll((unsigned long long)m) - 1;
       m &= m - 1;
       const int e = bit + 64 * i;
-      const float c = contract_dot<XC>(xv, nxc, p.router_w + (size_t)e * p.H);
+      const float c = RQ ? q8_contract_dot(xv, p.rq, (size_t)e, p.H)
+                         : contract_dot<XC>(xv, nxc, p.router_w + (size_t)e * p.H);
       if (lane == bit) out[i] = round_bf16(c);
     }
   }
-  const bool has_sg = p.sgate_w != nullptr;
-  const float sg_logit = has_sg ? contract_dot<XC>(xv, nxc, p.sgate_w) : 0.0f;
+  float sg_logit = 0.0f;
+  if (p.has_sg)
+    sg_logit = RQ ? q8_contract_dot(xv, p.sgq, 0, p.H) : contract_dot<XC>(xv, nxc, p.sgate_w);
   finish_route<P>(p, t, out, sg_logit, s_topk[wave]);
 }
 
@@ -696,22 +872,41 @@ bool router_mfma_eligible(int E, int H) {
   return E % 64 == 0 && E <= 256 && H % 512 == 0 && H <= 4096;
 }
 
-hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, hipStream_t s) {
-  hipLaunchKernelGGL(router_rownorm_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, wnorm);
-  if (a.T >= 4096)
-    hipLaunchKernelGGL(router_logits64_kernel, dim3((a.T + 63) / 64, a.E / 64), dim3(64), 0, s,
-                       a);
-  else
-    hipLaunchKernelGGL(router_logits16_kernel, dim3((a.T + 15) / 16, a.E / 64), dim3(64), 0, s,
-                       a);
-  hipLaunchKernelGGL(router_select_kernel, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                     (const float*)wnorm);
+hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split,
+                              hipStream_t s) {
+  const dim3 g16((a.T + 15) / 16, a.E / 64), g64((a.T + 63) / 64, a.E / 64);
+  const bool wide = a.T >= 4096;
+  if (a.rq8) {
+    // logits over the hi plane, then continued over the lo plane
+    hipLaunchKernelGGL(router_split_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, split,
+                       split + (size_t)a.E * a.H, wnorm);
+    DecodeArgs hi = a, lo = a;
+    hi.router_w = split;
+    lo.router_w = split + (size_t)a.E * a.H;
+    if (wide) {
+      hipLaunchKernelGGL(router_logits64_kernel<false>, g64, dim3(64), 0, s, hi);
+      hipLaunchKernelGGL(router_logits64_kernel<true>, g64, dim3(64), 0, s, lo);
+    } else {
+      hipLaunchKernelGGL(router_logits16_kernel<false>, g16, dim3(64), 0, s, hi);
+      hipLaunchKernelGGL(router_logits16_kernel<true>, g16, dim3(64), 0, s, lo);
+    }
+    hipLaunchKernelGGL(router_select_kernel<1>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                       (const float*)wnorm);
+  } else {
+    hipLaunchKernelGGL(router_rownorm_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, wnorm);
+    if (wide)
+      hipLaunchKernelGGL(router_logits64_kernel<false>, g64, dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL(router_logits16_kernel<false>, g16, dim3(64), 0, s, a);
+    hipLaunchKernelGGL(router_select_kernel<0>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                       (const float*)wnorm);
+  }
   RMOE_CHECK_LAUNCH();
   return hipSuccess;
 }
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
-  const int rows = a.E + (a.sgate_w ? 1 : 0);
+  const int rows = a.E + a.has_sg;
   dim3 grid((rows + 3) / 4, a.T);
   if (a.E <= 256)
     hipLaunchKernelGGL(router_kernel<4>, grid, dim3(256), 0, s, a);

@@ -5,8 +5,9 @@
 // grid, see launch_fused_decode).  Per layer:
 //
 //   R  router rows: the waves of each XCD compute every router row once
-//      (the fixed-order dot of the router contract) and publish it in that
-//      XCD's L2 only; the row weights are loaded before x is even staged
+//      (the fixed-order dot of the router contract; bf16 rows, or 8-bit
+//      MLX-affine rows with their group scales and biases) and publish it in
+//      that XCD's L2 only; the row weights are loaded before x is even staged
 //   K  every workgroup polls its XCD's logits (an L2 round trip, about half
 //      the latency of the device-coherent hand-overs) and ranks them with the
 //      shared gate's logit, which its wave 0 computes itself (row weights
@@ -247,6 +248,85 @@ __device__ __forceinline__ void load_down_words(DownRegs<Shape<BITS>::DN_WPL>& r
   }
 }
 
+// One gate row held in registers by a wave: bf16 (RQ 0: lane chunks
+// lane + 64 i of 8 values) or 8-bit MLX-affine (RQ 1: lane chunks of 16
+// codes with their group's scale and bias as raw bf16 bits).
+template <int RQ>
+struct GateRow;
+template <>
+struct GateRow<0> {
+  static constexpr int C = kFusedH / 8 / 64;
+  uint4 w[C];
+};
+template <>
+struct GateRow<1> {
+  static constexpr int C = kFusedH / 16 / 64;
+  uint4 w[C];
+  uint32_t s[C], b[C];
+};
+
+__device__ __forceinline__ void load_gate_row(GateRow<0>& r, const uint16_t* w, const QW&,
+                                              size_t, int lane) {
+#pragma unroll
+  for (int i = 0; i < GateRow<0>::C; ++i) r.w[i] = load16_stream(w + (lane + 64 * i) * 8);
+}
+__device__ __forceinline__ void load_gate_row(GateRow<1>& r, const uint16_t*, const QW& bank,
+                                              size_t row, int lane) {
+  constexpr int H = kFusedH;
+#pragma unroll
+  for (int i = 0; i < GateRow<1>::C; ++i) {
+    const int ch = lane + 64 * i;
+    r.w[i] = load16_stream(bank.w + row * (H / 4) + ch * 4);
+    r.s[i] = bank.s[row * (H / 64) + (ch >> 2)];
+    r.b[i] = bank.b[row * (H / 64) + (ch >> 2)];
+  }
+}
+
+// This lane's partial of the router contract's dot (x as floats in LDS).
+__device__ __forceinline__ float gate_partial(const GateRow<0>& r, const float* s_x, int lane) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < GateRow<0>::C; ++i) {
+    const float* xv = s_x + (lane + 64 * i) * 8;
+    acc = fmaf(xv[0], bf16_lo(r.w[i].x), acc);
+    acc = fmaf(xv[1], bf16_hi(r.w[i].x), acc);
+    acc = fmaf(xv[2], bf16_lo(r.w[i].y), acc);
+    acc = fmaf(xv[3], bf16_hi(r.w[i].y), acc);
+    acc = fmaf(xv[4], bf16_lo(r.w[i].z), acc);
+    acc = fmaf(xv[5], bf16_hi(r.w[i].z), acc);
+    acc = fmaf(xv[6], bf16_lo(r.w[i].w), acc);
+    acc = fmaf(xv[7], bf16_hi(r.w[i].w), acc);
+  }
+  return acc;
+}
+__device__ __forceinline__ float gate_partial(const GateRow<1>& r, const float* s_x, int lane) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < GateRow<1>::C; ++i) {
+    const float* xp = s_x + (lane + 64 * i) * 16;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) {
+      const float4 f = *reinterpret_cast<const float4*>(xp + j);
+      v[j] = f.x;
+      v[j + 1] = f.y;
+      v[j + 2] = f.z;
+      v[j + 3] = f.w;
+    }
+    acc = qgate_chunk(acc, r.w[i], v, bf16_to_f32(r.s[i]), bf16_to_f32(r.b[i]));
+  }
+  return acc;
+}
+
+// Whether the layer's shared expert has a sigmoid gate (its row pointer is
+// set).  Taken from the layer descriptor rather than a launch-wide flag: the
+// per-layer test keeps the compiler's schedule of the layer loop (a uniform
+// kernel-argument flag here cost about 1 us per layer).
+template <int RQ>
+__device__ __forceinline__ bool shared_gated(const FusedLayer& L, bool has_shared) {
+  return has_shared && (RQ ? L.sgq.w != nullptr : L.sgate_w != nullptr);
+}
+
 // Keep the compiler from moving loads or their uses across this point, so
 // that every load of a batch is issued before the first wait on any of them.
 __device__ __forceinline__ void issue_fence() {
@@ -260,22 +340,15 @@ __device__ __forceinline__ void issue_fence() {
 // first part is issued right after the current layer's routed loads and
 // the second after the current layer's down projection, so neither delays
 // a hand-over.
-template <int BITS, int RC>
+template <int BITS, int RQ>
 __device__ __forceinline__ void issue_router_and_shared_down(
-    const FusedLayer& L, int row, int n_rows, int E, bool has_shared, int h, int lane,
-    bool sg_wave, uint4 (&rw)[RC], uint4 (&sw)[RC], DownRegs<Shape<BITS>::DN_WPL>& drs,
+    const FusedLayer& L, int row, int n_rows, bool has_shared, int h, int lane,
+    bool sg_wave, GateRow<RQ>& rw, GateRow<RQ>& sw, DownRegs<Shape<BITS>::DN_WPL>& drs,
     uint32_t& dpws) {
   using S = Shape<BITS>;
   constexpr int H = S::H;
-  if (row < n_rows) {
-    const uint16_t* wr = row < E ? L.router_w + (size_t)row * H : L.sgate_w;
-#pragma unroll
-    for (int i = 0; i < RC; ++i) rw[i] = load16_stream(wr + (lane + 64 * i) * 8);
-  }
-  if (sg_wave && has_shared && L.sgate_w) {
-#pragma unroll
-    for (int i = 0; i < RC; ++i) sw[i] = load16_stream(L.sgate_w + (lane + 64 * i) * 8);
-  }
+  if (row < n_rows) load_gate_row(rw, L.router_w + (size_t)row * H, L.rq, (size_t)row, lane);
+  if (sg_wave && shared_gated<RQ>(L, has_shared)) load_gate_row(sw, L.sgate_w, L.sgq, 0, lane);
   if (has_shared && h < H) {
     if (lane < 8) dpws = load_down_param_word<BITS>(L.sdn, h, lane);
     load_down_words<BITS>(drs, L.sdn, h, lane);
@@ -304,7 +377,7 @@ __device__ __forceinline__ void issue_shared_pairs(const FusedLayer& L, bool has
   issue_fence();
 }
 
-template <int BITS>
+template <int BITS, int RQ>
 __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs p) {
   using S = Shape<BITS>;
   constexpr int H = S::H;
@@ -315,7 +388,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   constexpr int NU = kMaxFusedUnits;
   constexpr int kStageX = H / kThreads;                     // 4
   constexpr int kPer = kFusedMaxExperts / 64;               // keys per lane (4)
-  constexpr int RC = H / 8 / 64;                            // router chunks per lane
   static_assert(kPer == 4, "the local sort network below is for 4 keys per lane");
   static_assert(H % (256 * kXPollWaves) == 0 && NU * I % (256 * kActPollWaves) == 0,
                 "hand-overs split evenly over the polling waves");
@@ -354,10 +426,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   PairRegs<CPL> pr[NP];
   DownRegs<S::DN_WPL> dr[NU];      // slot NU-1: the shared unit
   uint32_t dpw0 = 0, dpw1 = 0;
-  uint4 rw[RC], sw[RC];  // router row; shared gate row (wave kPollWave)
+  GateRow<RQ> rw, sw;  // router row; shared gate row (wave kPollWave)
   {
     const FusedLayer L0 = p.table ? p.table[0] : p.layer0;
-    issue_router_and_shared_down<BITS, RC>(L0, row, E, E, p.has_shared, h, lane0,
+    issue_router_and_shared_down<BITS, RQ>(L0, row, E, p.has_shared, h, lane0,
                                            wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
     issue_shared_pairs<BITS, CPL, NP>(L0, p.has_shared, K, pw, n_waves, n_pairs, lane0, pr);
   }
@@ -379,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     const uint32_t tag_act = base + phase + 2;
     const uint32_t tag_x = base + phase + 3;  // used when a next layer reads x
     phase += last ? 2 : 3;
-    const bool sg_row = p.has_shared && L.sgate_w;
+    const bool sg_row = shared_gated<RQ>(L, p.has_shared);
 
     // ---- x (bf16 -> fp32 in LDS).  A chained layer collects the previous
     // layer's tagged output.
@@ -395,20 +467,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 
     // ---- R: this wave's router row.
     if (row < E) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < RC; ++i) {
-        const float* xv = s_x + (lane + 64 * i) * 8;
-        acc = fmaf(xv[0], bf16_lo(rw[i].x), acc);
-        acc = fmaf(xv[1], bf16_hi(rw[i].x), acc);
-        acc = fmaf(xv[2], bf16_lo(rw[i].y), acc);
-        acc = fmaf(xv[3], bf16_hi(rw[i].y), acc);
-        acc = fmaf(xv[4], bf16_lo(rw[i].z), acc);
-        acc = fmaf(xv[5], bf16_hi(rw[i].z), acc);
-        acc = fmaf(xv[6], bf16_lo(rw[i].w), acc);
-        acc = fmaf(xv[7], bf16_hi(rw[i].w), acc);
-      }
-      acc = wave_sum(acc);
+      const float acc = wave_sum(gate_partial(rw, s_x, lane));
       if (lane == 0)
         __builtin_amdgcn_raw_buffer_store_b32(
             tagged(f32_to_bf16(acc), tag_logit),
@@ -420,22 +479,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     if (wave == kPollWave) {
       // the shared gate's logit, computed here (its row is not handed over)
       uint32_t wsg = 0;
-      if (sg_row) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < RC; ++i) {
-          const float* xv = s_x + (lane + 64 * i) * 8;
-          acc = fmaf(xv[0], bf16_lo(sw[i].x), acc);
-          acc = fmaf(xv[1], bf16_hi(sw[i].x), acc);
-          acc = fmaf(xv[2], bf16_lo(sw[i].y), acc);
-          acc = fmaf(xv[3], bf16_hi(sw[i].y), acc);
-          acc = fmaf(xv[4], bf16_lo(sw[i].z), acc);
-          acc = fmaf(xv[5], bf16_hi(sw[i].z), acc);
-          acc = fmaf(xv[6], bf16_lo(sw[i].w), acc);
-          acc = fmaf(xv[7], bf16_hi(sw[i].w), acc);
-        }
-        wsg = f32_to_bf16(wave_sum(acc)) << 16;
-      }
+      if (sg_row) wsg = f32_to_bf16(wave_sum(gate_partial(sw, s_x, lane))) << 16;
       // lane l holds experts 4 l .. 4 l + 3 (one 16-byte load from the L2)
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           sc->logits[xcd], (short)0, E * 4, 0x00020000);
@@ -669,7 +713,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     // extra loads (shared gate row, shared pairs) are back by then.
     if (!last) {
       const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
-      issue_router_and_shared_down<BITS, RC>(Ln, row, E, E, p.has_shared, h, lane,
+      issue_router_and_shared_down<BITS, RQ>(Ln, row, E, p.has_shared, h, lane,
                                              wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
       issue_shared_pairs<BITS, CPL, NP>(Ln, p.has_shared, K, pw, n_waves, n_pairs, lane, pr);
     }
@@ -682,13 +726,21 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   if (wg == 0 && threadIdx.x == 0) store_coherent_u32(&sc->epoch, base + phase);
 }
 
-hipError_t fused_grid(int bits, int* grid) {
+namespace {
+const void* fused_fn(int bits, int rq8) {
+  if (bits == 8)
+    return rq8 ? (const void*)fused_decode_kernel<8, 1> : (const void*)fused_decode_kernel<8, 0>;
+  return rq8 ? (const void*)fused_decode_kernel<4, 1> : (const void*)fused_decode_kernel<4, 0>;
+}
+}  // namespace
+
+hipError_t fused_grid(int bits, int rq8, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   // Occupancy does not change for a device: cache it (grid + 1, 0 = unknown).
-  static int cache[64][2];
-  const int slot = bits == 8 ? 0 : 1;
+  static int cache[64][4];
+  const int slot = (bits == 8 ? 0 : 2) + (rq8 ? 1 : 0);
   if (dev >= 0 && dev < 64) {
     const int c = __atomic_load_n(&cache[dev][slot], __ATOMIC_RELAXED);
     if (c > 0) {
@@ -700,10 +752,7 @@ hipError_t fused_grid(int bits, int* grid) {
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   int per_cu = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      &per_cu,
-      bits == 8 ? (const void*)fused_decode_kernel<8> : (const void*)fused_decode_kernel<4>,
-      kThreads, 0);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_fn(bits, rq8), kThreads, 0);
   if (e != hipSuccess) return e;
   *grid = per_cu >= 1 ? (cus < kFusedMaxGrid ? cus : kFusedMaxGrid) : 0;
   if (dev >= 0 && dev < 64) __atomic_store_n(&cache[dev][slot], *grid + 1, __ATOMIC_RELAXED);
@@ -713,18 +762,14 @@ hipError_t fused_grid(int bits, int* grid) {
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s) {
   FusedArgs args = a;
   void* kargs[] = {&args};
-  const void* fn = bits == 8 ? (const void*)fused_decode_kernel<8>
-                             : (const void*)fused_decode_kernel<4>;
+  const void* fn = fused_fn(bits, a.rq8);
   // A cooperative launch guarantees every workgroup is resident.  Under
   // stream capture a plain launch of the same one-workgroup-per-CU grid is
   // recorded instead (every workgroup fits at once on an otherwise idle
   // device; the bounded waits turn anything else into a status error).
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
-    hipLaunchKernelGGL((bits == 8 ? fused_decode_kernel<8> : fused_decode_kernel<4>),
-                       dim3(grid), dim3(kThreads), 0, s, args);
-    return hipGetLastError();
-  }
+  if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+    return hipLaunchKernel(fn, dim3(grid), dim3(kThreads), kargs, 0, s);
   return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kThreads), kargs, 0, s);
 }
 

@@ -26,9 +26,12 @@ struct QW {
 struct DecodeArgs {
   int T, H, I, E, K, has_shared, norm;
   int switch_mode;   // 1: idx are caller indices, range-checked per use
+  int rq8;           // 1: the gates are 8-bit MLX-affine banks (rq, sgq)
+  int has_sg;        // the shared expert has a sigmoid gate (sgate_w or sgq)
   const uint16_t* x;
-  const uint16_t* router_w;
+  const uint16_t* router_w;   // bf16 gates (rq8 == 0)
   const uint16_t* sgate_w;
+  QW rq, sgq;                 // quantized gates [E, H] / [1, H] (rq8 == 1)
   QW gu, dn, sgu, sdn;
   float* logits;     // [T, E + 1]
   int32_t* idx;      // [T, K]   (switch path: caller's indices)
@@ -66,6 +69,7 @@ struct FusedLayer {
   const uint16_t* router_w;
   const uint16_t* sgate_w;
   QW gu, dn, sgu, sdn;
+  QW rq, sgq;                 // 8-bit gates when the call's rq8 is set
 };
 
 // Device scratch of the fused kernel: lives at a fixed workspace offset so
@@ -82,6 +86,7 @@ struct FusedScratch {
 
 struct FusedArgs {
   int n_layers, E, K, norm, has_shared;
+  int rq8;                    // gates are 8-bit MLX-affine (every layer)
   int residual_mode;          // 0 none, 1 the layer input, 2 `residual`
   FusedLayer layer0;          // used when table == nullptr
   const FusedLayer* table;    // device array of n_layers descriptors
@@ -93,13 +98,15 @@ struct FusedArgs {
   float* scores_out;
 };
 
-hipError_t fused_grid(int bits, int* grid);
+hipError_t fused_grid(int bits, int rq8, int* grid);
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s);
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s);
 // Many-token router on the matrix cores with exact selection (prefill).
 bool router_mfma_eligible(int E, int H);
-hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, hipStream_t s);
+// wnorm: [E] floats; split: [2, E, H] bf16 (quantized gates only)
+hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split,
+                              hipStream_t s);
 hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s);
 hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s);
 hipError_t launch_qmv(const QmvArgs& a, int bits, hipStream_t s);

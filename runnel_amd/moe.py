@@ -130,24 +130,46 @@ def fuse_routed_gate_up(model) -> int:
     return count
 
 
+def _gate_linear(hidden_size: int, rows: int, gate_bits: int | None, group_size: int, device):
+    if gate_bits is None:
+        return Linear(hidden_size, rows, device=device)
+    return QuantizedLinear(hidden_size, rows, bits=gate_bits, group_size=group_size,
+                           device=device)
+
+
+def _gate_operand(gate):
+    """What the kernels take for a gate module: the bf16 weight, or the
+    (weight, scales, biases) triple of an 8-bit group-64 affine gate; None
+    for any other format."""
+    if isinstance(gate, QuantizedLinear):
+        if gate.bits != 8 or gate.group_size != 64 or gate.mode != "affine":
+            return None
+        return (gate.weight, gate.scales, gate.biases)
+    return gate.weight
+
+
 class SparseMoeBlock(nn.Module):
-    """Router + routed experts + sigmoid-gated shared expert."""
+    """Router + routed experts + sigmoid-gated shared expert.  ``gate_bits``
+    quantizes the router ``gate`` and ``shared_expert_gate`` (8 in real
+    checkpoints: bench/runnel_bench/checkpoint.py:200-208); None keeps them
+    bf16."""
 
     def __init__(self, hidden_size: int, moe_intermediate_size: int, num_experts: int,
                  num_experts_per_tok: int, shared_expert_intermediate_size: int | None = None,
                  norm_topk_prob: bool = True, bits: int = 8, group_size: int = 64,
-                 device=None):
+                 device=None, gate_bits: int | None = None):
         super().__init__()
         self.num_experts = num_experts
         self.top_k = num_experts_per_tok
         self.norm_topk_prob = norm_topk_prob
-        self.gate = Linear(hidden_size, num_experts, device=device)
+        self.gate = _gate_linear(hidden_size, num_experts, gate_bits, group_size, device)
         self.switch_mlp = SwitchGLU(hidden_size, moe_intermediate_size, num_experts,
                                     bits=bits, group_size=group_size, device=device)
         if shared_expert_intermediate_size:
             self.shared_expert = MLP(hidden_size, shared_expert_intermediate_size, bits,
                                      group_size, device=device)
-            self.shared_expert_gate = Linear(hidden_size, 1, device=device)
+            self.shared_expert_gate = _gate_linear(hidden_size, 1, gate_bits, group_size,
+                                                   device)
         else:
             self.shared_expert = None
             self.shared_expert_gate = None
@@ -162,6 +184,9 @@ class SparseMoeBlock(nn.Module):
         sm = self.switch_mlp
         if not isinstance(sm, FusedQuantizedSwitchGLU) or not sm._fast_path():
             return None
+        router = _gate_operand(self.gate)
+        if router is None:
+            return None
         shared = None
         sgate = None
         if self.shared_expert is not None:
@@ -175,10 +200,12 @@ class SparseMoeBlock(nn.Module):
                    torch.cat([se.up_proj.scales, se.gate_proj.scales], 0).contiguous(),
                    torch.cat([se.up_proj.biases, se.gate_proj.biases], 0).contiguous())
             shared = (sgu, (se.down_proj.weight, se.down_proj.scales, se.down_proj.biases))
-            sgate = self.shared_expert_gate.weight.reshape(-1)
+            sgate = _gate_operand(self.shared_expert_gate)
+            if sgate is None or type(self.shared_expert_gate) is not type(self.gate):
+                return None
         dp = sm.down_proj
         self._handle = native.make_layer(
-            self.gate.weight, (sm.weight, sm.scales, sm.biases),
+            router, (sm.weight, sm.scales, sm.biases),
             (dp.weight, dp.scales, dp.biases), self.top_k, self.norm_topk_prob,
             shared_gate_w=sgate,
             shared_gate_up=None if shared is None else shared[0],
@@ -201,7 +228,10 @@ class SparseMoeBlock(nn.Module):
         D = x.shape[-1]
         lead = x.shape[:-1]
         x2 = x.reshape(-1, D)
-        inds, scores = native.router(self.gate.weight, x2, self.top_k, self.norm_topk_prob)
+        router = _gate_operand(self.gate)
+        if router is None:
+            raise ValueError("router gate must be bf16 or 8-bit group-64 affine")
+        inds, scores = native.router(router, x2, self.top_k, self.norm_topk_prob)
         y = self.switch_mlp(x2, inds)  # [T, k, D]
         out = (y.float() * scores[..., None]).sum(dim=-2)
         if self.shared_expert is not None:

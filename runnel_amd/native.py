@@ -154,14 +154,30 @@ class LayerHandle:
         _lib.check(_lib.load().rmoe_validate_layer(ctypes.byref(self.struct)))
 
 
+def _gate(g, rows: int | None, name: str):
+    """A router / shared gate: a bf16 tensor, or a (weight, scales, biases)
+    triple of an 8-bit group-64 quantized gate -> (bf16 tensor or None,
+    rmoe_qweight, tensors to keep alive)."""
+    if isinstance(g, (tuple, list)):
+        w, s, b = (t.reshape(-1, t.shape[-1]).contiguous() for t in g)
+        if rows is not None and w.shape[0] != rows:
+            raise ValueError(f"{name} must have {rows} rows (got {w.shape[0]})")
+        return None, qweight_struct(w, s, b, 8, 64), (w, s, b)
+    return g, _lib.QWeight(), ()
+
+
 def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
                shared_gate_w=None, shared_gate_up=None, shared_down=None,
                bits: int = 8, group_size: int = 64) -> LayerHandle:
-    """router_w bf16 [E, H]; gate_up / down / shared_* are (weight, scales,
-    biases) triples of packed banks; shared banks may omit the expert axis."""
+    """router_w bf16 [E, H], or the (weight, scales, biases) triple of an
+    8-bit group-64 quantized gate (QuantizedLinear); shared_gate_w likewise
+    (bf16 [H] or a one-row triple, in the router's format); gate_up / down /
+    shared_* are (weight, scales, biases) triples of packed banks; shared
+    banks may omit the expert axis."""
     gu = qweight_struct(*gate_up, bits, group_size)
     dn = qweight_struct(*down, bits, group_size)
-    keep = [router_w, *gate_up, *down]
+    router_w, rq, rkeep = _gate(router_w, None, "router gate")
+    keep = [*rkeep, *gate_up, *down]
     if shared_gate_up is not None:
         sgu = qweight_struct(*shared_gate_up, bits, group_size)
         sdn = qweight_struct(*shared_down, bits, group_size)
@@ -171,14 +187,22 @@ def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
         sgu = _lib.QWeight()
         sdn = _lib.QWeight()
         shared_inter = 0
+    sgq = _lib.QWeight()
     if shared_gate_w is not None:
-        shared_gate_w = shared_gate_w.reshape(-1).contiguous()
-        keep.append(shared_gate_w)
-    if router_w.dtype != BF16 or not router_w.is_contiguous():
-        raise ValueError("router weight must be contiguous bfloat16 [experts, hidden]")
-    s = _lib.Layer(router_w.shape[1], gu.rows // 2, shared_inter, router_w.shape[0],
-                   top_k, int(bool(norm_topk_prob)), router_w.data_ptr(),
-                   _lib.ptr(shared_gate_w), gu, dn, sgu, sdn)
+        shared_gate_w, sgq, skeep = _gate(shared_gate_w, 1, "shared gate")
+        keep += list(skeep)
+        if shared_gate_w is not None:
+            shared_gate_w = shared_gate_w.reshape(-1).contiguous()
+            keep.append(shared_gate_w)
+    if router_w is not None:
+        if router_w.dtype != BF16 or not router_w.is_contiguous():
+            raise ValueError("router weight must be contiguous bfloat16 [experts, hidden]")
+        keep.append(router_w)
+        E, H = router_w.shape
+    else:
+        E, H = rq.rows, rq.cols
+    s = _lib.Layer(H, gu.rows // 2, shared_inter, E, top_k, int(bool(norm_topk_prob)),
+                   _lib.ptr(router_w), _lib.ptr(shared_gate_w), gu, dn, sgu, sdn, rq, sgq)
     h = LayerHandle(s, tuple(keep))
     h.validate()
     return h
@@ -255,23 +279,31 @@ def workspace_status(ws: torch.Tensor) -> int:
     return int(ws[off:off + 4].view(torch.int32).item())
 
 
-def router(router_w: torch.Tensor, x: torch.Tensor, top_k: int,
-           norm_topk_prob: bool = True):
-    """Router of the block: x bf16 [T, H], router_w bf16 [E, H] ->
+def router(router_w, x: torch.Tensor, top_k: int, norm_topk_prob: bool = True):
+    """Router of the block: x bf16 [T, H], router_w bf16 [E, H] or the
+    (weight, scales, biases) triple of an 8-bit group-64 quantized gate ->
     (indices int32 [T, k] in rank order, scores float32 [T, k])."""
     lib = _lib.load()
-    _require_cuda(x, router_w)
     x = x.contiguous()
-    router_w = router_w.contiguous()
     T, H = x.shape
-    E = router_w.shape[0]
+    w, rq, keep = _gate(router_w, None, "router gate")
+    _require_cuda(x, w, *keep)
+    E = rq.rows if w is None else w.shape[0]
     idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     scores = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
     need = lib.rmoe_router_workspace_bytes(E, top_k, T)
     ws = WORKSPACE.get(x.device, need, "router")
-    _lib.check(lib.rmoe_router(router_w.data_ptr(), E, H, top_k, int(bool(norm_topk_prob)),
-                               x.data_ptr(), T, idx.data_ptr(), scores.data_ptr(),
-                               ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device)))
+    if w is None:
+        if rq.cols != H:
+            raise ValueError(f"router gate has {rq.cols} columns, x has {H}")
+        _lib.check(lib.rmoe_router_q(ctypes.byref(rq), top_k, int(bool(norm_topk_prob)),
+                                     x.data_ptr(), T, idx.data_ptr(), scores.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device)))
+    else:
+        w = w.contiguous()
+        _lib.check(lib.rmoe_router(w.data_ptr(), E, H, top_k, int(bool(norm_topk_prob)),
+                                   x.data_ptr(), T, idx.data_ptr(), scores.data_ptr(),
+                                   ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device)))
     return idx, scores
 
 

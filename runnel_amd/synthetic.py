@@ -3,7 +3,9 @@
 Weights are drawn from N(0, std) with a seeded torch generator on the
 device, quantized by the HIP quantizer (rmoe_quantize) in chunks, and kept
 resident: a 256-expert 8-bit layer is 0.86 GB, so the 40-layer stack is
-34 GB of HBM.  The router and the shared-expert gate stay bf16.
+34 GB of HBM.  The router and the shared-expert gate are bf16, or 8-bit
+group-64 (weight, scales, biases) triples with ``gate_bits=8`` (the format
+of real checkpoints).
 """
 
 from __future__ import annotations
@@ -19,10 +21,10 @@ BF16 = torch.bfloat16
 
 @dataclass
 class LayerWeights:
-    router_w: torch.Tensor        # bf16 [E, H]
+    router_w: "torch.Tensor | tuple"  # bf16 [E, H] or an 8-bit triple [E, ...]
     gate_up: tuple                # (int32 [E, 2I, H/vpw], bf16 [E, 2I, H/64] x2)
     down: tuple                   # (int32 [E, H, I/vpw], ...)
-    shared_gate_w: torch.Tensor | None
+    shared_gate_w: "torch.Tensor | tuple | None"  # bf16 [H] or an 8-bit triple [1, ...]
     shared_gate_up: tuple | None  # [2Is, H/vpw] ...
     shared_down: tuple | None
     bits: int
@@ -35,9 +37,11 @@ class LayerWeights:
                                  self.shared_gate_up, self.shared_down, self.bits)
 
     def tensors(self):
-        ts = [self.router_w, *self.gate_up, *self.down]
+        def flat(g):
+            return list(g) if isinstance(g, tuple) else [g]
+        ts = [*flat(self.router_w), *self.gate_up, *self.down]
         if self.shared_gate_up is not None:
-            ts += [self.shared_gate_w, *self.shared_gate_up, *self.shared_down]
+            ts += [*flat(self.shared_gate_w), *self.shared_gate_up, *self.shared_down]
         return ts
 
     def nbytes(self) -> int:
@@ -65,11 +69,19 @@ def _quantized_bank(gen, experts, rows, cols, bits, std, device, chunk_rows=1 <<
 
 def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8, bits=8,
                shared=True, std=0.02, router_std=0.02, device="cuda",
-               shared_inter=None) -> LayerWeights:
+               shared_inter=None, gate_bits=None) -> LayerWeights:
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     shared_inter = inter if shared_inter is None else shared_inter
-    router = (torch.randn((experts, hidden), generator=gen, device=device) * router_std).to(BF16)
+
+    def gate(shape):
+        w = torch.randn(shape, generator=gen, device=device) * router_std
+        if gate_bits is None:
+            return w.to(BF16)
+        return tuple(t.reshape(-1 if len(shape) > 1 else 1, t.shape[-1])
+                     for t in native.quantize(w.reshape(-1, hidden), gate_bits))
+
+    router = gate((experts, hidden))
     gu = _quantized_bank(gen, experts, 2 * inter, hidden, bits, std, device)
     dn = _quantized_bank(gen, experts, hidden, inter, bits, std, device)
     if gu[0].dim() == 2:  # experts == 1 keeps the expert axis for banks
@@ -77,7 +89,7 @@ def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8, bits=8,
         dn = tuple(t.unsqueeze(0) for t in dn)
     sg = sgu = sdn = None
     if shared:
-        sg = (torch.randn((hidden,), generator=gen, device=device) * router_std).to(BF16)
+        sg = gate((hidden,))
         sgu = _quantized_bank(gen, 1, 2 * shared_inter, hidden, bits, std, device)
         sdn = _quantized_bank(gen, 1, hidden, shared_inter, bits, std, device)
     return LayerWeights(router, gu, dn, sg, sgu, sdn, bits, top_k)
@@ -108,7 +120,10 @@ def zipf_bias(seed: int, experts: int, s: float = 1.1, alpha: float = 0.8,
 
 
 def apply_router_bias(layer: LayerWeights, bias: torch.Tensor) -> None:
-    """Route `bias` through input feature 0 (inputs from make_skewed_x)."""
+    """Route `bias` through input feature 0 (inputs from make_skewed_x).
+    A bf16 router only."""
+    if isinstance(layer.router_w, tuple):
+        raise ValueError("router bias needs a bf16 router")
     layer.router_w[:, 0] = (bias / BIAS_FEATURE).to(BF16)
 
 

@@ -70,6 +70,109 @@ def test_validate_layer_accepts_and_rejects():
     assert lib.rmoe_validate_layer(ctypes.byref(bad)) == _lib.RMOE_EBITS
 
 
+def _qlayer(E=4, H=256, I=64, K=2, shared=True):
+    """A layer with 8-bit quantized router and shared gate."""
+    L = _layer(8, E, H, I, K, shared)
+    L.router_w = None
+    L.shared_gate_w = None
+    L.router_q = _qw(8, 1, E, H)
+    if shared:
+        L.shared_gate_q = _qw(8, 1, 1, H)
+    return L
+
+
+def test_layer_struct_matches_the_header():
+    """The Python mirror of rmoe_layer has the C layout: the quantized gates
+    sit after the four banks (fields appended in ABI version 2)."""
+    q = ctypes.sizeof(_lib.QWeight)
+    assert q == 3 * 8 + 5 * 4 + 4          # three pointers, five int32, padding
+    assert _lib.Layer.router_q.offset == _lib.Layer.gate_up.offset + 4 * q
+    assert _lib.Layer.shared_gate_q.offset == _lib.Layer.router_q.offset + q
+    text = (ROOT / "include" / "rmoe.h").read_text()
+    body = text[text.index("typedef struct rmoe_layer"):text.index("} rmoe_layer;")]
+    names = re.findall(r"(\w+);", body)
+    assert names == [f[0] for f in _lib.Layer._fields_]
+
+
+def test_validate_quantized_gates():
+    lib = _lib.load()
+    assert lib.rmoe_validate_layer(ctypes.byref(_qlayer())) == _lib.RMOE_OK
+    assert lib.rmoe_validate_layer(ctypes.byref(_qlayer(shared=False))) == _lib.RMOE_OK
+    both = _qlayer()
+    both.router_w = FAKE
+    assert lib.rmoe_validate_layer(ctypes.byref(both)) == _lib.RMOE_EINVAL
+    assert b"exactly one of router_w" in lib.rmoe_last_error()
+    neither = _layer()
+    neither.router_w = None
+    assert lib.rmoe_validate_layer(ctypes.byref(neither)) == _lib.RMOE_ENULL
+    four = _qlayer()
+    four.router_q.bits = 4
+    four.router_q.cols = 256
+    assert lib.rmoe_validate_layer(ctypes.byref(four)) == _lib.RMOE_EBITS
+    assert b"must be 8-bit" in lib.rmoe_last_error()
+    rows = _qlayer()
+    rows.router_q.rows = 5
+    assert lib.rmoe_validate_layer(ctypes.byref(rows)) == _lib.RMOE_EINVAL
+    mixed = _qlayer()
+    mixed.shared_gate_q = _lib.QWeight()
+    mixed.shared_gate_w = FAKE
+    assert lib.rmoe_validate_layer(ctypes.byref(mixed)) == _lib.RMOE_EINVAL
+    assert b"router's format" in lib.rmoe_last_error()
+    mixed = _layer()
+    mixed.shared_gate_q = _qw(8, 1, 1, 256)
+    mixed.shared_gate_w = None
+    assert lib.rmoe_validate_layer(ctypes.byref(mixed)) == _lib.RMOE_EINVAL
+    sg = _qlayer()
+    sg.shared_gate_q.rows = 2
+    assert lib.rmoe_validate_layer(ctypes.byref(sg)) == _lib.RMOE_EINVAL
+    no_shared = _qlayer(shared=False)
+    no_shared.shared_gate_q = _qw(8, 1, 1, 256)
+    assert lib.rmoe_validate_layer(ctypes.byref(no_shared)) == _lib.RMOE_EINVAL
+
+
+def test_quantized_router_rejects_before_launch():
+    lib = _lib.load()
+    r = _qw(8, 1, 16, 256)
+    need = lib.rmoe_router_workspace_bytes(16, 2, 3)
+    assert lib.rmoe_router_q(None, 2, 1, FAKE, 3, FAKE, FAKE, FAKE, need, None) == _lib.RMOE_ENULL
+    assert lib.rmoe_router_q(ctypes.byref(r), 17, 1, FAKE, 3, FAKE, FAKE, FAKE, need,
+                             None) == _lib.RMOE_EINVAL
+    assert lib.rmoe_router_q(ctypes.byref(r), 2, 1, FAKE + 2, 3, FAKE, FAKE, FAKE, need,
+                             None) == _lib.RMOE_EALIGN
+    assert lib.rmoe_router_q(ctypes.byref(r), 2, 1, FAKE, 3, FAKE, FAKE, FAKE, need - 1,
+                             None) == _lib.RMOE_EWS
+    r4 = _qw(4, 1, 16, 256)
+    assert lib.rmoe_router_q(ctypes.byref(r4), 2, 1, FAKE, 3, FAKE, FAKE, FAKE, need,
+                             None) == _lib.RMOE_EBITS
+    bank = _qw(8, 2, 16, 256)
+    assert lib.rmoe_router_q(ctypes.byref(bank), 2, 1, FAKE, 3, FAKE, FAKE, FAKE, need,
+                             None) == _lib.RMOE_EINVAL
+    assert lib.rmoe_router_q(ctypes.byref(r), 2, 1, FAKE, 0, None, None, None, 0,
+                             None) == _lib.RMOE_OK
+
+
+def test_quantized_gate_prefill_workspace_holds_the_split_planes():
+    """A call that takes the matrix-core router needs room for the two bf16
+    planes of an 8-bit gate (2 * E * H * 2 bytes) beyond the bf16 layout."""
+    lib = _lib.load()
+    T = 256
+    bf = lib.rmoe_workspace_bytes(ctypes.byref(_layer(E=64, H=512, I=128, K=4)), T)
+    q = lib.rmoe_workspace_bytes(ctypes.byref(_qlayer(E=64, H=512, I=128, K=4)), T)
+    assert q - bf >= 2 * 64 * 512 * 2
+    assert lib.rmoe_workspace_bytes(ctypes.byref(_qlayer(E=64, H=512, I=128, K=4)), 1) == \
+        lib.rmoe_workspace_bytes(ctypes.byref(_layer(E=64, H=512, I=128, K=4)), 1)
+
+
+def test_chain_table_pack_rejects_mixed_gate_formats():
+    lib = _lib.load()
+    layers = (_lib.Layer * 2)(_layer(H=2048, I=512, E=256, K=8),
+                              _qlayer(H=2048, I=512, E=256, K=8))
+    n = lib.rmoe_chain_table_bytes(2)
+    buf = (ctypes.c_uint8 * n)()
+    assert lib.rmoe_chain_table_pack(layers, 2, ctypes.addressof(buf)) == _lib.RMOE_EINVAL
+    assert b"layer 1 differs" in lib.rmoe_last_error()
+
+
 def test_block_rejects_before_launch():
     lib = _lib.load()
     L = _layer()
@@ -137,6 +240,7 @@ def test_chain_table_pack_rejects_mixed_layers():
     n = lib.rmoe_chain_table_bytes(2)
     buf = (ctypes.c_uint8 * n)()
     assert lib.rmoe_chain_table_pack(layers, 2, ctypes.addressof(buf)) == _lib.RMOE_EINVAL
+    assert b"layer 1 differs" in lib.rmoe_last_error()
     assert lib.rmoe_chain_table_bytes(0) == 0
 
 

@@ -3,6 +3,8 @@ mathematics or an independent implementation fixes (not a retyped formula):
 known packed words, brute force on tiny inputs, the C restatement of the
 reference's own oracle, invariants of top-k / softmax / the permutation."""
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -261,3 +263,136 @@ def test_prefill_mode_close_to_contract(bits):
     fa, fb = M.bf16_to_f32(a), M.bf16_to_f32(b)
     assert not np.array_equal(a, b)
     assert np.abs(fa - fb).max() <= 4 * 2.0 ** -8 * max(np.abs(fa).max(), 1e-3)
+
+
+# ---------------------------------------------------------------- quantized gate
+
+
+def _c_fmaf(a, b, c):
+    lib = M.c_oracle()
+    a, b, c = (np.ascontiguousarray(v, dtype=np.float32) for v in (a, b, c))
+    out = np.empty_like(a)
+    lib.orc_fmaf_array(M._p(a), M._p(b), M._p(c), M._p(out), a.size)
+    return out
+
+
+def test_fma32_matches_c_fmaf():
+    """Random operands over a wide exponent range, plus operands built so
+    that a*b + c lies just off a float32 rounding midpoint by less than a
+    float64 ulp: there a plain float64 sum rounds twice and lands on the
+    wrong neighbour, which the C library's fmaf does not."""
+    rng = np.random.default_rng(40)
+    n = 20000
+    a = (rng.standard_normal(n) * 2.0 ** rng.integers(-30, 30, n)).astype(np.float32)
+    b = (rng.standard_normal(n) * 2.0 ** rng.integers(-30, 30, n)).astype(np.float32)
+    c = (rng.standard_normal(n) * 2.0 ** rng.integers(-60, 60, n)).astype(np.float32)
+    assert np.array_equal(M.fma32(a, b, c).view(np.uint32), _c_fmaf(a, b, c).view(np.uint32))
+    # a*b = 2^6 (1 - 2^-46); c = 2^30 + 2^7 (odd last bit): the exact sum is
+    # just below the midpoint 2^30 + 2^7 + 2^6
+    ha = np.float32(64.0 * (1.0 + 2.0 ** -23))
+    hb = np.float32(1.0 - 2.0 ** -23)
+    hc = np.float32(2.0 ** 30 + 2.0 ** 7)
+    sa = np.array([ha, -ha, ha, -ha], np.float32)
+    sb = np.array([hb, hb, -hb, -hb], np.float32)
+    sc = np.array([hc, -hc, -hc, hc], np.float32)
+    want = _c_fmaf(sa, sb, sc)
+    assert np.array_equal(M.fma32(sa, sb, sc).view(np.uint32), want.view(np.uint32))
+    naive = (sa.astype(np.float64) * sb + sc).astype(np.float32)
+    assert not np.array_equal(naive, want)       # the case really needs the fix
+    assert want[0] == np.float32(2.0 ** 30 + 2.0 ** 7)
+
+
+def _qgate(rng, rows, H, bits, std=0.02):
+    w = (rng.standard_normal((rows, H)) * std).astype(np.float32)
+    words, s, b = M.quantize(w, bits)
+    return M.QWeight(words[None], s[None], b[None], bits)
+
+
+@pytest.mark.parametrize("bits,H", [(8, 2048), (4, 2048), (8, 512), (8, 320)])
+def test_qrouter_logits_equal_c_restatement(bits, H):
+    """Bit-equal to the C restatement (libm fmaf) for full rows, rows of
+    fewer than 64 chunks, and a row whose last lane round is partial."""
+    rng = np.random.default_rng(41 + bits + H)
+    x = M.f32_to_bf16(rng.standard_normal((3, H)).astype(np.float32))
+    q = _qgate(rng, 12, H, bits)
+    got = M.qrouter_logits(x, q)
+    lib = M.c_oracle()
+    keep = []
+    cq = M._cqw(q, keep)
+    c = np.array([[lib.orc_qrouter_dot(ctypes.byref(cq), e, M._p(np.ascontiguousarray(x[t])))
+                   for e in range(12)] for t in range(3)], np.float32)
+    assert np.array_equal(got.view(np.uint32), c.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_qrouter_logits_within_rounding_bound_of_exact(bits):
+    """|contract - exact| <= gamma_n * sum_k |x_k| (|q_k s| + |b|) with n
+    the roundings a term passes through (V - 1 in its chunk, two per chunk
+    in its lane, six in the butterfly); the exact value is x . deq(W) in
+    float64.  The error is not zero (fp32 sums really happen)."""
+    rng = np.random.default_rng(50 + bits)
+    H = 2048
+    x = M.f32_to_bf16(rng.standard_normal((4, H)).astype(np.float32))
+    q = _qgate(rng, 64, H, bits)
+    got = M.qrouter_logits(x, q).astype(np.float64)
+    xf = M.bf16_to_f32(x).astype(np.float64)
+    exact = xf @ q.dequant(0).T
+    codes = M.unpack(q.w[0], bits).astype(np.float64)
+    s = np.repeat(M.bf16_to_f32(q.scales[0]).astype(np.float64), 64, axis=-1)
+    b = np.repeat(M.bf16_to_f32(q.biases[0]).astype(np.float64), 64, axis=-1)
+    mag = np.abs(xf) @ (np.abs(codes * s) + np.abs(b)).T
+    V = 128 // bits
+    n = (V - 1) + 2 * (H // V // 64) + 6
+    bound = n * 2.0 ** -24 / (1 - n * 2.0 ** -24) * mag
+    err = np.abs(got - exact)
+    assert np.all(err <= bound)
+    assert err.max() > 0
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_qrouter_logits_exact_on_integer_data(bits):
+    """Small-integer inputs, power-of-two scales that differ per group and
+    integer biases: every partial sum is an exactly representable integer,
+    so the contract value is the exact integer dot.  A dropped bias term,
+    a wrong group index or a wrong nibble order would not be."""
+    rng = np.random.default_rng(60 + bits)
+    H, E = 1024, 9
+    codes = rng.integers(0, 1 << bits, size=(E, H)).astype(np.uint32)
+    groups = H // 64
+    s = (2.0 ** rng.integers(-2, 3, size=(E, groups))).astype(np.float32)
+    b = rng.integers(-8, 9, size=(E, groups)).astype(np.float32)
+    q = M.QWeight(M.pack(codes, bits)[None], M.f32_to_bf16(s)[None], M.f32_to_bf16(b)[None], bits)
+    xi = rng.integers(-3, 4, size=(5, H)).astype(np.float32)
+    x = M.f32_to_bf16(xi)
+    got = M.qrouter_logits(x, q).astype(np.float64)
+    w = codes * np.repeat(s, 64, axis=1).astype(np.float64) + np.repeat(b, 64, axis=1)
+    assert np.array_equal(got, xi.astype(np.float64) @ w.T)
+
+
+def test_quantized_gate_block_numpy_and_c_agree():
+    """The whole block with 8-bit router and shared gate through both
+    restatements: identical routing and shared gate, same outputs."""
+    L = M.make_layer(70, hidden=512, inter=128, experts=32, top_k=4, bits=8, router_bits=8)
+    assert isinstance(L.router_w, M.QWeight) and isinstance(L.shared_gate_w, M.QWeight)
+    x = M.make_x(71, 6, 512)
+    a, ia, sa = M.block_forward(L, x, residual_bits=x)
+    b, ib, sb = M.c_block_forward(L, x, residual_bits=x)
+    assert np.array_equal(ia, ib)
+    assert np.abs(sa - sb).max() <= 2.0 ** -8
+    diff = np.abs(M.bf16_to_f32(a) - M.bf16_to_f32(b))
+    assert (a == b).mean() > 0.98
+    assert diff.max() <= np.abs(M.bf16_to_f32(a)).max() * 2.0 ** -6
+
+
+def test_quantized_gate_routes_like_its_dequantised_bf16_gate_mostly():
+    """An 8-bit gate is a close approximation of the float gate it was
+    quantized from: the selections mostly agree (a sanity check that the
+    codes, scales and biases are read as the layout says)."""
+    Lq = M.make_layer(72, hidden=1024, inter=64, experts=64, top_k=8, bits=8, router_bits=8,
+                      shared=False)
+    x = M.make_x(73, 32, 1024)
+    iq, _, _ = M.route(x, Lq.router_w, 8)
+    wf = M.f32_to_bf16(Lq.router_w.dequant(0).astype(np.float32))
+    ib, _, _ = M.route(x, wf, 8)
+    same = np.mean([len(set(a) & set(b)) / 8 for a, b in zip(iq, ib)])
+    assert same > 0.9
