@@ -40,17 +40,21 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "MoE layer µs/token + achieved HBM GB/s, 8-bit bs=1 decode; prefill tok/s"
 
 
-def layer_bytes(hidden, inter, experts, top_k, bits, shared=True, tokens=1, residual=False):
+def layer_bytes(hidden, inter, experts, top_k, bits, shared=True, tokens=1, residual=False,
+                gate_bits=None):
     """Algorithmic HBM bytes of one decode step of one layer: every selected
     expert's packed gate/up and down weights with their bf16 scales and
-    biases, the shared expert, the bf16 router, the shared gate vector, the
-    input, the output (and the residual read when chained)."""
+    biases, the shared expert, the router, the shared gate vector (bf16, or
+    packed 8-bit codes with their scales and biases), the input, the output
+    (and the residual read when chained)."""
     gu = 2 * inter * hidden * bits // 8 + 2 * inter * (hidden // 64) * 4
     dn = hidden * inter * bits // 8 + hidden * (inter // 64) * 4
     per_expert = gu + dn
-    b = top_k * per_expert + experts * hidden * 2
+    gate_row = (hidden * 2 if gate_bits is None
+                else hidden * gate_bits // 8 + (hidden // 64) * 4)
+    b = top_k * per_expert + experts * gate_row
     if shared:
-        b += per_expert + hidden * 2
+        b += per_expert + gate_row
     b += tokens * hidden * 2 * (3 if residual else 2)
     return b
 
@@ -114,11 +118,11 @@ def cpu_baseline(lw, x_host, budget_s: float = 12.0):
     return median(times), threads, len(times)
 
 
-def build_stack(n_layers, bits, seed0=0):
+def build_stack(n_layers, bits, seed0=0, gate_bits=None):
     from runnel_amd import synthetic
     layers = []
     for l in range(n_layers):
-        layers.append(synthetic.make_layer(seed0 + l, bits=bits))
+        layers.append(synthetic.make_layer(seed0 + l, bits=bits, gate_bits=gate_bits))
     return layers
 
 
@@ -129,7 +133,7 @@ def run_decode_chain(args, torch):
     n_layers = args.layers
     bits = args.bits
     t0 = time.perf_counter()
-    stack = build_stack(n_layers, bits)
+    stack = build_stack(n_layers, bits, gate_bits=args.gate_bits)
     chain = native.Chain([lw.handle() for lw in stack])
     torch.cuda.synchronize()
     gen_s = time.perf_counter() - t0
@@ -177,7 +181,7 @@ def run_decode_chain(args, torch):
     total_us = ev[0].elapsed_time(ev[-1]) * 1000.0
     us_token = total_us / args.steps
     us_layer = us_token / n_layers
-    lbytes = layer_bytes(H, 512, 256, 8, bits, residual=True)
+    lbytes = layer_bytes(H, 512, 256, 8, bits, residual=True, gate_bits=args.gate_bits)
     gbps = lbytes / (us_layer * 1e-6) / 1e9
     return {
         "us_layer": us_layer, "us_token": us_token, "step_us": step_us, "gbps": gbps,
@@ -246,6 +250,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--bits", type=int, default=8)
+    ap.add_argument("--gate-bits", type=int, choices=[8], default=None,
+                    help="quantize the router and shared gate to 8 bits (the real "
+                         "checkpoints' format); default bf16 gates")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
@@ -280,7 +287,7 @@ def main():
     res = run_decode_chain(args, torch)
     launch_bytes = res["layer_bytes"] * args.layers
     achieved = launch_bytes / (res["us_token"] * 1e-6) / 1e9
-    traffic = recorded_traffic(args.layers, args.bits)
+    traffic = recorded_traffic(args.layers, args.bits) if args.gate_bits is None else None
     out = {
         "metric": METRIC,
         "value": round(res["us_layer"], 3),
@@ -298,6 +305,7 @@ def main():
             "workload": f"{args.layers}-layer {args.bits}-bit MoE chain, batch-1 decode with "
                         "residual (hidden 2048, 256 experts, top-8 + shared, inter 512, group 64)",
             "layers": args.layers, "bits": args.bits, "tokens_per_step": 1,
+            "gates": "bf16" if args.gate_bits is None else f"{args.gate_bits}-bit affine",
             "launch": args.launch,
             "resident_weight_gb": round(res["resident_gb"], 2),
         },

@@ -348,3 +348,7 @@ def test_bench_byte_model_matches_the_survey_figures():
     import bench
     assert bench.layer_bytes(2048, 512, 256, 8, 8) == 31_141_888
     assert bench.layer_bytes(2048, 512, 256, 8, 4) == 16_986_112
+    # 8-bit gates: 256 rows of 2048 codes + 32 (scale, bias) pairs, and one
+    # such row for the shared gate, instead of 257 bf16 rows
+    q = bench.layer_bytes(2048, 512, 256, 8, 8, gate_bits=8)
+    assert 31_141_888 - q == 257 * (4096 - (2048 + 128))
