@@ -137,7 +137,9 @@ int rmoe_router_q(const rmoe_qweight* router, int32_t top_k, int32_t norm_topk_p
  * (token, slot) the packed [up; gate] projection of expert indices[t, j],
  * SwiGLU, then the expert's down projection.  y bf16 [tokens, top_k,
  * hidden], per slot and not combined.  A slot whose index is outside
- * [0, experts) yields a zero row and touches no weight memory. */
+ * [0, experts) yields a zero row and touches no weight memory.  From 64
+ * (token, slot) rows on (the expert-sorted path) y must be 16-byte
+ * aligned. */
 int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
                     const uint16_t* x, int32_t tokens, const int32_t* indices,
                     int32_t top_k, uint16_t* y, void* workspace,
@@ -145,6 +147,24 @@ int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
 size_t rmoe_switch_workspace_bytes(const rmoe_qweight* gate_up,
                                    const rmoe_qweight* down, int32_t tokens,
                                    int32_t top_k);
+
+/* The routed half of the block for a caller's routing: the experts of
+ * rmoe_switch_glu, then out[t] = bf16(sum_j weights[t, j] * y[t, j]) in slot
+ * order, with residual != NULL out[t] = bf16(residual[t] + out[t]).  mlx-lm's
+ * `(switch_mlp(x, inds) * scores[..., None]).sum(-2)` (the caller of
+ * src/runnel/mlx.py:57-82), and the reference's native two-stage MoE with
+ * given router weights (native/src/fused_moe_probe.mm:494-537, the
+ * RNLMOE01 datasets of bench/export_ornith_moe_layer.py).  weights fp32
+ * [tokens, top_k]; a slot with an out-of-range index adds nothing; out bf16
+ * [tokens, hidden], not aliasing x. */
+int rmoe_switch_combine(const rmoe_qweight* gate_up, const rmoe_qweight* down,
+                        const uint16_t* x, int32_t tokens, const int32_t* indices,
+                        const float* weights, int32_t top_k, const uint16_t* residual,
+                        uint16_t* out, void* workspace, size_t workspace_bytes,
+                        void* stream);
+size_t rmoe_switch_combine_workspace_bytes(const rmoe_qweight* gate_up,
+                                           const rmoe_qweight* down, int32_t tokens,
+                                           int32_t top_k);
 
 /* gather_qmm(x, w, scales, biases, rhs_indices, transpose=True):
  * y[m] = x[lhs[m]] . deq(w[rhs[m]])^T for m < rows.  lhs_indices == NULL
@@ -160,7 +180,9 @@ int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows,
  * score_j * y_j + bf16(sigmoid(x . shared_gate_w)) * y_shared); with
  * residual != NULL, out[t] = bf16(residual[t] + out[t]).  indices_out /
  * scores_out may be NULL.  x, residual, out bf16 [tokens, hidden]; out may
- * alias residual but not x. */
+ * alias residual but not x.  Calls that route 64 or more (token, slot) rows
+ * take the expert-sorted path, which needs out and residual 16-byte
+ * aligned (2 bytes otherwise). */
 int rmoe_moe_block(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
                    const uint16_t* residual, uint16_t* out,
                    int32_t* indices_out, float* scores_out, void* workspace,

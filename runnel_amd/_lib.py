@@ -30,6 +30,7 @@ EXPORTED = (
     "rmoe_moe_block", "rmoe_quantize", "rmoe_dequantize", "rmoe_stream_read",
     "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes", "rmoe_chain_table_pack",
     "rmoe_moe_chain", "rmoe_workspace_status_offset", "rmoe_router_q",
+    "rmoe_switch_combine", "rmoe_switch_combine_workspace_bytes",
 )
 
 
@@ -103,6 +104,9 @@ def load() -> ctypes.CDLL:
         lib.rmoe_router_workspace_bytes.restype = SZ
         lib.rmoe_router_workspace_bytes.argtypes = [I32, I32, I32]
         lib.rmoe_switch_glu.argtypes = [QP, QP, P, I32, P, I32, P, P, SZ, P]
+        lib.rmoe_switch_combine.argtypes = [QP, QP, P, I32, P, P, I32, P, P, P, SZ, P]
+        lib.rmoe_switch_combine_workspace_bytes.restype = SZ
+        lib.rmoe_switch_combine_workspace_bytes.argtypes = [QP, QP, I32, I32]
         lib.rmoe_gather_qmm.argtypes = [P, I32, P, P, I32, QP, P, P, P]
         lib.rmoe_moe_block.argtypes = [LP, P, I32, P, P, P, P, P, SZ, P]
         lib.rmoe_quantize.argtypes = [P, I64, I32, I32, I32, P, P, P, P]
@@ -117,6 +121,7 @@ def load() -> ctypes.CDLL:
         for name in EXPORTED:
             if name not in ("rmoe_last_error", "rmoe_status_string",
                             "rmoe_workspace_bytes", "rmoe_switch_workspace_bytes",
+                            "rmoe_switch_combine_workspace_bytes",
                             "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes",
                             "rmoe_workspace_status_offset"):
                 getattr(lib, name).restype = ctypes.c_int

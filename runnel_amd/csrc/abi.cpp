@@ -256,6 +256,7 @@ rmoe::PrefillArgs prefill_args(const Layout& l, void* ws, int T, int H, int I, i
   a.act = reinterpret_cast<uint16_t*>(base + l.act16);
   a.y = l.y16 ? reinterpret_cast<uint16_t*>(base + l.y16) : nullptr;
   a.scores = reinterpret_cast<const float*>(base + l.scores);
+  a.score_stride = K + 1;
   return a;
 }
 
@@ -304,6 +305,7 @@ rmoe::DecodeArgs decode_args(const rmoe_layer* L, const uint16_t* x, int T,
   a.logits = reinterpret_cast<float*>(base + l.logits);
   a.idx = reinterpret_cast<int32_t*>(base + l.idx);
   a.scores = reinterpret_cast<float*>(base + l.scores);
+  a.score_stride = a.K + 1;
   a.act = reinterpret_cast<float*>(base + l.act);
   a.ctr = reinterpret_cast<uint32_t*>(base + l.ctr);
   return a;
@@ -360,6 +362,93 @@ rmoe::FusedArgs fused_args(const rmoe_layer* L, const uint16_t* x, uint16_t* out
   return f;
 }
 
+// Shapes shared by the switch calls: gate_up [E, 2I, H], down [E, H, I].
+int check_switch(const rmoe_qweight* gate_up, const rmoe_qweight* down, int32_t tokens,
+                 int32_t top_k) {
+  int rc;
+  if ((rc = check_qweight(gate_up, "gate_up"))) return rc;
+  if ((rc = check_qweight(down, "down"))) return rc;
+  if ((rc = check_tokens(tokens))) return rc;
+  if (gate_up->rows % 2) return fail(RMOE_EINVAL, "gate_up rows must be 2*inter");
+  const int I = gate_up->rows / 2;
+  const int H = gate_up->cols;
+  if (down->experts != gate_up->experts || down->rows != H || down->cols != I)
+    return fail(RMOE_EINVAL, "down must be [experts, hidden, inter] of gate_up");
+  if (down->bits != gate_up->bits)
+    return fail(RMOE_EBITS, "gate_up and down must share one bit width");
+  if ((rc = check_down_width(I, down->bits, "down"))) return rc;
+  if (top_k < 1 || top_k > rmoe::kMaxTopK)
+    return fail(RMOE_EINVAL, "top_k must be in [1, %d] (got %d)", rmoe::kMaxTopK, top_k);
+  return RMOE_OK;
+}
+
+// The routed experts for caller indices; `weights` == nullptr: per-slot
+// outputs into y [T, K, H]; otherwise out[t] = bf16(sum_j w[t, j] y[t, j])
+// (+ residual) into y [T, H].
+int switch_call(const rmoe_qweight* gate_up, const rmoe_qweight* down, const uint16_t* x,
+                int32_t tokens, const int32_t* indices, const float* weights, int32_t top_k,
+                const uint16_t* residual, uint16_t* y, void* ws, size_t ws_bytes,
+                void* stream) {
+  int rc;
+  if ((rc = check_switch(gate_up, down, tokens, top_k))) return rc;
+  if (tokens == 0) return ok();
+  const bool combine = weights != nullptr;
+  if (!x || !indices || !y) return fail(RMOE_ENULL, "x, indices and the output are required");
+  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  const int I = gate_up->rows / 2;
+  const int H = gate_up->cols;
+  const bool sorted = prefill_path(tokens, top_k, gate_up->experts, H, I);
+  // the sorted path moves output and residual rows in 16-byte pieces
+  const size_t row_align = sorted ? 16 : 2;
+  if (!aligned(indices, 4) || (combine && !aligned(weights, 4)))
+    return fail(RMOE_EALIGN, "indices/weights must be 4-byte aligned");
+  if (!aligned(y, row_align) || (residual && !aligned(residual, row_align)))
+    return fail(RMOE_EALIGN, "output/residual must be %zu-byte aligned", row_align);
+  if (combine && static_cast<const void*>(y) == static_cast<const void*>(x))
+    return fail(RMOE_EINVAL, "out must not alias x");
+  const Layout lay = layout(tokens, gate_up->experts, top_k, I, H, sorted, combine);
+  if ((rc = check_ws(ws, ws_bytes, lay.total))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (sorted) {
+    rmoe::PrefillArgs pa = prefill_args(lay, ws, tokens, H, I, gate_up->experts, top_k, x,
+                                        indices);
+    pa.gu = qw(*gate_up);
+    pa.dn = qw(*down);
+    if (combine) {
+      pa.scores = weights;
+      pa.score_stride = top_k;
+      pa.residual = residual;
+      pa.out = y;
+    } else {
+      pa.y = y;
+    }
+    const hipError_t e = rmoe::launch_prefill(pa, gate_up->bits, combine, s);
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return ok();
+  }
+  rmoe_layer L{};
+  L.hidden = H;
+  L.inter = I;
+  L.experts = gate_up->experts;
+  L.top_k = top_k;
+  L.gate_up = *gate_up;
+  L.down = *down;
+  rmoe::DecodeArgs a = decode_args(&L, x, tokens, ws);
+  a.idx = const_cast<int32_t*>(indices);
+  a.switch_mode = 1;
+  a.out = y;
+  if (combine) {
+    a.scores = const_cast<float*>(weights);
+    a.score_stride = top_k;
+    a.residual = residual;
+  }
+  hipError_t e = rmoe::launch_gate_up(a, gate_up->bits, s);
+  if (e != hipSuccess) return hip_fail(e, "gate/up launch");
+  e = rmoe::launch_down(a, gate_up->bits, combine, s);
+  if (e != hipSuccess) return hip_fail(e, "down launch");
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -399,6 +488,16 @@ size_t rmoe_switch_workspace_bytes(const rmoe_qweight* gate_up,
   const int H = gate_up->cols;
   const bool sorted = prefill_path(tokens, top_k, gate_up->experts, H, I);
   return layout(tokens, gate_up->experts, top_k, I, H, sorted, false).total;
+}
+
+size_t rmoe_switch_combine_workspace_bytes(const rmoe_qweight* gate_up,
+                                           const rmoe_qweight* down, int32_t tokens,
+                                           int32_t top_k) {
+  if (!gate_up || !down || tokens < 0 || top_k < 1) return 0;
+  const int I = gate_up->rows / 2;
+  const int H = gate_up->cols;
+  const bool sorted = prefill_path(tokens, top_k, gate_up->experts, H, I);
+  return layout(tokens, gate_up->experts, top_k, I, H, sorted, true).total;
 }
 
 size_t rmoe_router_workspace_bytes(int32_t experts, int32_t top_k, int32_t tokens) {
@@ -490,6 +589,10 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   if (static_cast<const void*>(out) == static_cast<const void*>(x))
     return fail(RMOE_EINVAL, "out must not alias x");
   const Layout lay = block_layout(L, tokens);
+  if (lay.rows && (!aligned(out, 16) || (residual && !aligned(residual, 16))))
+    return fail(RMOE_EALIGN,
+                "out/residual must be 16-byte aligned for calls that route %d or more "
+                "(token, slot) rows", rmoe::kPrefillMinRows);
   if ((rc = check_ws(ws, ws_bytes, lay.total))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int bits = L->gate_up.bits;
@@ -544,55 +647,17 @@ int rmoe_switch_glu(const rmoe_qweight* gate_up, const rmoe_qweight* down,
                     const uint16_t* x, int32_t tokens, const int32_t* indices,
                     int32_t top_k, uint16_t* y, void* ws, size_t ws_bytes,
                     void* stream) {
-  int rc;
-  if ((rc = check_qweight(gate_up, "gate_up"))) return rc;
-  if ((rc = check_qweight(down, "down"))) return rc;
-  if ((rc = check_tokens(tokens))) return rc;
-  if (gate_up->rows % 2) return fail(RMOE_EINVAL, "gate_up rows must be 2*inter");
-  const int I = gate_up->rows / 2;
-  const int H = gate_up->cols;
-  if (down->experts != gate_up->experts || down->rows != H || down->cols != I)
-    return fail(RMOE_EINVAL, "down must be [experts, hidden, inter] of gate_up");
-  if (down->bits != gate_up->bits)
-    return fail(RMOE_EBITS, "gate_up and down must share one bit width");
-  if ((rc = check_down_width(I, down->bits, "down"))) return rc;
-  if (top_k < 1 || top_k > rmoe::kMaxTopK)
-    return fail(RMOE_EINVAL, "top_k must be in [1, %d] (got %d)", rmoe::kMaxTopK, top_k);
-  if (tokens == 0) return ok();
-  if (!x || !indices || !y) return fail(RMOE_ENULL, "x, indices and y are required");
-  if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
-  if (!aligned(indices, 4) || !aligned(y, 2))
-    return fail(RMOE_EALIGN, "indices/y misaligned");
-  const bool sorted = prefill_path(tokens, top_k, gate_up->experts, H, I);
-  const Layout lay = layout(tokens, gate_up->experts, top_k, I, H, sorted, false);
-  if ((rc = check_ws(ws, ws_bytes, lay.total))) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (sorted) {
-    rmoe::PrefillArgs pa = prefill_args(lay, ws, tokens, H, I, gate_up->experts, top_k, x,
-                                        indices);
-    pa.gu = qw(*gate_up);
-    pa.dn = qw(*down);
-    pa.y = y;
-    const hipError_t e = rmoe::launch_prefill(pa, gate_up->bits, false, s);
-    if (e != hipSuccess) return hip_fail(e, "prefill launch");
-    return ok();
-  }
-  rmoe_layer L{};
-  L.hidden = H;
-  L.inter = I;
-  L.experts = gate_up->experts;
-  L.top_k = top_k;
-  L.gate_up = *gate_up;
-  L.down = *down;
-  rmoe::DecodeArgs a = decode_args(&L, x, tokens, ws);
-  a.idx = const_cast<int32_t*>(indices);
-  a.switch_mode = 1;
-  a.out = y;
-  hipError_t e = rmoe::launch_gate_up(a, gate_up->bits, s);
-  if (e != hipSuccess) return hip_fail(e, "gate/up launch");
-  e = rmoe::launch_down(a, gate_up->bits, false, s);
-  if (e != hipSuccess) return hip_fail(e, "down launch");
-  return ok();
+  return switch_call(gate_up, down, x, tokens, indices, nullptr, top_k, nullptr, y, ws,
+                     ws_bytes, stream);
+}
+
+int rmoe_switch_combine(const rmoe_qweight* gate_up, const rmoe_qweight* down,
+                        const uint16_t* x, int32_t tokens, const int32_t* indices,
+                        const float* weights, int32_t top_k, const uint16_t* residual,
+                        uint16_t* out, void* ws, size_t ws_bytes, void* stream) {
+  if (tokens > 0 && !weights) return fail(RMOE_ENULL, "weights are required");
+  return switch_call(gate_up, down, x, tokens, indices, weights, top_k, residual, out, ws,
+                     ws_bytes, stream);
 }
 
 int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows, const int32_t* lhs,

@@ -780,7 +780,7 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
       float y = sv[b] * qdot_chunk<BITS>(wv[b], a) + bv[b] * asum;
       y = round_bf16(segment_sum_fast(y, CHR));
       if constexpr (COMBINE) {
-        acc += p.scores[t * (p.K + 1) + u] * y;
+        acc += p.scores[t * p.score_stride + u] * y;
       } else {
         if (ch == 0 && valid)
           p.out[((size_t)t * p.K + u) * H + h] = (uint16_t)f32_to_bf16(y);

@@ -35,7 +35,8 @@ struct DecodeArgs {
   QW gu, dn, sgu, sdn;
   float* logits;     // [T, E + 1]
   int32_t* idx;      // [T, K]   (switch path: caller's indices)
-  float* scores;     // [T, K + 1] (slot K: shared sigmoid gate)
+  float* scores;     // [T, score_stride] (router: K + 1, slot K = shared gate)
+  int score_stride;  // K + 1 (the router's scores) or K (caller weights)
   float* act;        // [T, K + has_shared, I]
   uint32_t* ctr;     // [T] zero between calls
   uint16_t* out;     // [T, H] (block) or [T, K, H] (switch)
@@ -139,7 +140,8 @@ struct PrefillArgs {
   int32_t* hist;           // [sort slices][E + 2] rows per bucket of each slice
   uint16_t* act;           // [T K + T, I] bf16, sorted order
   uint16_t* y;             // [T K (+ T), H] bf16 at row t K + j (shared: T K + t)
-  const float* scores;     // [T, K + 1] router scores, slot K = shared gate
+  const float* scores;     // [T, score_stride] router scores, slot K = shared gate
+  int score_stride;        // K + 1 (the router's) or K (caller weights, no shared)
   const uint16_t* residual;
   uint16_t* out;           // [T, H]
 };

@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs 
   const int H = p.H;
   const int K = p.K;
   const int units = K + p.has_shared;
-  const float* sc = p.scores + (size_t)t * (K + 1);
+  const float* sc = p.scores + (size_t)t * p.score_stride;
   for (int h0 = threadIdx.x * 8; h0 < H; h0 += 256 * 8) {
     float acc[8];
 #pragma unroll

@@ -133,6 +133,32 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate_up: _lib.QWeight,
     return y
 
 
+def switch_combine(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor,
+                   gate_up: _lib.QWeight, down: _lib.QWeight,
+                   residual: torch.Tensor | None = None) -> torch.Tensor:
+    """The routed half of the block for a given routing: x bf16 [T, H],
+    indices int [T, k], weights float32 [T, k] -> bf16 [T, H] =
+    bf16(sum_j weights[t, j] * y[t, j]) (+ residual)."""
+    lib = _lib.load()
+    _require_cuda(x, indices, weights, residual)
+    x = x.contiguous()
+    idx = indices.to(torch.int32).contiguous()
+    w = weights.to(torch.float32).contiguous()
+    T, k = idx.shape
+    if tuple(w.shape) != (T, k):
+        raise ValueError(f"weights must be [{T}, {k}] (got {list(w.shape)})")
+    out = torch.empty((T, gate_up.cols), dtype=BF16, device=x.device)
+    res = None if residual is None else residual.contiguous()
+    need = lib.rmoe_switch_combine_workspace_bytes(ctypes.byref(gate_up), ctypes.byref(down),
+                                                   T, k)
+    ws = WORKSPACE.get(x.device, need, "switch")
+    _lib.check(lib.rmoe_switch_combine(ctypes.byref(gate_up), ctypes.byref(down),
+                                       x.data_ptr(), T, idx.data_ptr(), w.data_ptr(), k,
+                                       _lib.ptr(res), out.data_ptr(), ws.data_ptr(),
+                                       ws.numel(), _lib.stream_handle(x.device)))
+    return out
+
+
 @dataclass
 class LayerHandle:
     """An rmoe_layer struct plus the tensors it points at (kept alive)."""

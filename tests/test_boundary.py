@@ -220,6 +220,29 @@ def test_switch_and_qmm_reject_before_launch():
                                None) == _lib.RMOE_EINVAL
 
 
+def test_switch_combine_rejects_before_launch():
+    lib = _lib.load()
+    gu, dn = _qw(8, 4, 256, 256), _qw(8, 4, 256, 128)
+    need = lib.rmoe_switch_combine_workspace_bytes(ctypes.byref(gu), ctypes.byref(dn), 32, 2)
+    assert need > lib.rmoe_switch_workspace_bytes(ctypes.byref(gu), ctypes.byref(dn), 32, 2)
+    args = (ctypes.byref(gu), ctypes.byref(dn), FAKE, 32)
+    assert lib.rmoe_switch_combine(*args, FAKE, None, 2, None, FAKE + 4096, FAKE, need,
+                                   None) == _lib.RMOE_ENULL          # no weights
+    assert lib.rmoe_switch_combine(*args, FAKE, FAKE, 2, None, FAKE, FAKE, need,
+                                   None) == _lib.RMOE_EINVAL         # out aliases x
+    # 64 routed rows take the sorted path: 16-byte aligned rows required
+    assert lib.rmoe_switch_combine(*args, FAKE, FAKE, 2, None, FAKE + 4098, FAKE, need,
+                                   None) == _lib.RMOE_EALIGN
+    assert lib.rmoe_switch_combine(*args, FAKE, FAKE, 2, FAKE + 2, FAKE + 4096, FAKE, need,
+                                   None) == _lib.RMOE_EALIGN
+    assert lib.rmoe_switch_combine(*args, FAKE, FAKE, 2, None, FAKE + 4096, FAKE, need - 256,
+                                   None) == _lib.RMOE_EWS
+    assert lib.rmoe_switch_glu(*args, FAKE, 2, FAKE + 2, FAKE,
+                               lib.rmoe_switch_workspace_bytes(ctypes.byref(gu),
+                                                               ctypes.byref(dn), 32, 2),
+                               None) == _lib.RMOE_EALIGN
+
+
 def test_router_quantize_stream_reject_before_launch():
     lib = _lib.load()
     assert lib.rmoe_router(FAKE, 16, 100, 2, 1, FAKE, 1, FAKE, FAKE, FAKE, 1 << 20,
