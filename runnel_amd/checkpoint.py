@@ -94,18 +94,15 @@ class SafeTensorStore:
                 dtype = meta["dtype"]
                 shape = tuple(int(d) for d in meta["shape"])
                 b, e = (int(v) for v in meta["data_offsets"])
-                if dtype not in _DTYPES:
-                    info = None
-                else:
+                # tensors of other dtypes are indexed too; reading them fails
+                if dtype in _DTYPES:
                     nbytes = math.prod(shape) * _DTYPES[dtype][0].itemsize
                     if e - b != nbytes or b < 0 or data + e > size:
                         raise ValueError(f"tensor {name}: byte range [{b}, {e}) does not "
                                          f"match {dtype} {list(shape)} in {path.name}")
-                    info = TensorInfo(path, data + b, data + e, shape, dtype)
                 if name in self.entries:
                     raise ValueError(f"tensor {name} appears in more than one shard")
-                self.entries[name] = info if info is not None else TensorInfo(
-                    path, data + b, data + e, shape, dtype)
+                self.entries[name] = TensorInfo(path, data + b, data + e, shape, dtype)
 
     def __contains__(self, name: str) -> bool:
         return name in self.entries
