@@ -41,7 +41,7 @@ METRIC = "MoE layer µs/token + achieved HBM GB/s, 8-bit bs=1 decode; prefill to
 
 
 def layer_bytes(hidden, inter, experts, top_k, bits, shared=True, tokens=1, residual=False,
-                gate_bits=None):
+                gate_bits=None, post_norm=False):
     """Algorithmic HBM bytes of one decode step of one layer: every selected
     expert's packed gate/up and down weights with their bf16 scales and
     biases, the shared expert, the router, the shared gate vector (bf16, or
@@ -56,6 +56,8 @@ def layer_bytes(hidden, inter, experts, top_k, bits, shared=True, tokens=1, resi
     if shared:
         b += per_expert + gate_row
     b += tokens * hidden * 2 * (3 if residual else 2)
+    if post_norm:
+        b += hidden * 2   # the RMSNorm weights
     return b
 
 
@@ -118,11 +120,12 @@ def cpu_baseline(lw, x_host, budget_s: float = 12.0):
     return median(times), threads, len(times)
 
 
-def build_stack(n_layers, bits, seed0=0, gate_bits=None):
+def build_stack(n_layers, bits, seed0=0, gate_bits=None, post_norm=False):
     from runnel_amd import synthetic
     layers = []
     for l in range(n_layers):
-        layers.append(synthetic.make_layer(seed0 + l, bits=bits, gate_bits=gate_bits))
+        layers.append(synthetic.make_layer(seed0 + l, bits=bits, gate_bits=gate_bits,
+                                           post_norm=post_norm))
     return layers
 
 
@@ -133,7 +136,7 @@ def run_decode_chain(args, torch):
     n_layers = args.layers
     bits = args.bits
     t0 = time.perf_counter()
-    stack = build_stack(n_layers, bits, gate_bits=args.gate_bits)
+    stack = build_stack(n_layers, bits, gate_bits=args.gate_bits, post_norm=args.post_norm)
     chain = native.Chain([lw.handle() for lw in stack])
     torch.cuda.synchronize()
     gen_s = time.perf_counter() - t0
@@ -181,7 +184,8 @@ def run_decode_chain(args, torch):
     total_us = ev[0].elapsed_time(ev[-1]) * 1000.0
     us_token = total_us / args.steps
     us_layer = us_token / n_layers
-    lbytes = layer_bytes(H, 512, 256, 8, bits, residual=True, gate_bits=args.gate_bits)
+    lbytes = layer_bytes(H, 512, 256, 8, bits, residual=True, gate_bits=args.gate_bits,
+                         post_norm=args.post_norm)
     gbps = lbytes / (us_layer * 1e-6) / 1e9
     return {
         "us_layer": us_layer, "us_token": us_token, "step_us": step_us, "gbps": gbps,
@@ -253,6 +257,9 @@ def main():
     ap.add_argument("--gate-bits", type=int, choices=[8], default=None,
                     help="quantize the router and shared gate to 8 bits (the real "
                          "checkpoints' format); default bf16 gates")
+    ap.add_argument("--post-norm", action="store_true",
+                    help="put each layer's post-attention RMSNorm in front of its block "
+                         "(h + MoE(RMSNorm(h)), the decoder's sequence)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
@@ -287,7 +294,8 @@ def main():
     res = run_decode_chain(args, torch)
     launch_bytes = res["layer_bytes"] * args.layers
     achieved = launch_bytes / (res["us_token"] * 1e-6) / 1e9
-    traffic = recorded_traffic(args.layers, args.bits) if args.gate_bits is None else None
+    traffic = (recorded_traffic(args.layers, args.bits)
+               if args.gate_bits is None and not args.post_norm else None)
     out = {
         "metric": METRIC,
         "value": round(res["us_layer"], 3),
@@ -306,6 +314,7 @@ def main():
                         "residual (hidden 2048, 256 experts, top-8 + shared, inter 512, group 64)",
             "layers": args.layers, "bits": args.bits, "tokens_per_step": 1,
             "gates": "bf16" if args.gate_bits is None else f"{args.gate_bits}-bit affine",
+            "post_norm": bool(args.post_norm),
             "launch": args.launch,
             "resident_weight_gb": round(res["resident_gb"], 2),
         },

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define RMOE_ABI_VERSION 2
+#define RMOE_ABI_VERSION 3
 
 #define RMOE_OK 0
 #define RMOE_EINVAL (-1) /* inconsistent or unsupported shape / argument */
@@ -85,7 +85,13 @@ typedef struct rmoe_qweight {
  * gate then uses the same format: shared_gate_q [1, 1, hidden] instead of
  * shared_gate_w.  Quantized gate logits follow a fixed fp32 order of their
  * own: 16-code chunks lane + 64 i of a 64-lane wave, per chunk
- * acc = fma(sum q x, s, acc), acc = fma(sum x, b, acc), then a butterfly. */
+ * acc = fma(sum q x, s, acc), acc = fma(sum x, b, acc), then a butterfly.
+ *
+ * post_norm_w != NULL puts the decoder layer's post-attention RMSNorm in
+ * front of the block (appended in ABI version 3): the block's input is
+ * rmoe_rms_norm(x, post_norm_w, norm_eps), the residual stays what the
+ * caller passes, so a decoder computes h' = h + MoE(RMSNorm(h)) with
+ * residual = x = h (the layer sequence of docs/architecture.md:31-37). */
 typedef struct rmoe_layer {
   int32_t hidden;
   int32_t inter;
@@ -101,9 +107,19 @@ typedef struct rmoe_layer {
   rmoe_qweight shared_down;      /* [1, hidden, shared_inter] */
   rmoe_qweight router_q;         /* 8-bit gate [1, experts, hidden], or w NULL */
   rmoe_qweight shared_gate_q;    /* 8-bit shared gate [1, 1, hidden], or w NULL */
+  const uint16_t* post_norm_w;   /* bf16 [hidden] RMSNorm weights, or NULL */
+  float norm_eps;                /* its epsilon, in [0, 1] */
 } rmoe_layer;
 
 int rmoe_abi_version(void);
+
+/* RMSNorm of `tokens` rows (mx.fast.rms_norm(x, weight, eps); checkpoints
+ * store the effective weight): out = bf16(bf16(x r) w) with r = 1 /
+ * sqrt(sum(x^2) / hidden + eps), the sum in the router's fixed fp32 order,
+ * r correctly rounded.  hidden a multiple of 8; x, weight, out bf16, 16-byte
+ * aligned. */
+int rmoe_rms_norm(const uint16_t* x, const uint16_t* weight, int32_t tokens, int32_t hidden,
+                  float eps, uint16_t* out, void* stream);
 const char* rmoe_last_error(void);
 const char* rmoe_status_string(int status);
 

@@ -342,6 +342,9 @@ typedef struct {
                                     when router_w is NULL */
   orc_qweight shared_gate_q;     /* quantized shared gate [1, 1, hidden], used
                                     when shared_gate_w is NULL and w != NULL */
+  const uint16_t* post_norm_w;   /* bf16 [hidden]: RMSNorm of x before the
+                                    block, or NULL */
+  float norm_eps;
 } orc_layer;
 
 /*
@@ -409,6 +412,24 @@ float orc_qrouter_dot(const orc_qweight* qw, int row, const uint16_t* x) {
     memcpy(p, q, sizeof(p));
   }
   return p[0];
+}
+
+/*
+ * RMSNorm of one bf16 row in front of the block: s = sum x^2 in the router
+ * dot's order (orc_router_dot of x with itself; squares of bf16 values are
+ * exact), ms = s / H, v = ms + eps, r = 1 / sqrt(v) (each correctly rounded
+ * in fp32), out = bf16(bf16(x r) w).
+ */
+void orc_rms_norm(const uint16_t* x, const uint16_t* w, int hidden, float eps,
+                  uint16_t* out) {
+  const float s = orc_router_dot(x, x, hidden);
+  const float ms = s / (float)hidden;
+  const float v = ms + eps;
+  const float r = 1.0f / sqrtf(v);
+  for (int k = 0; k < hidden; ++k) {
+    const float n = round_bf16(orc_bf16_to_f32(x[k]) * r);
+    out[k] = orc_f32_to_bf16(n * orc_bf16_to_f32(w[k]));
+  }
 }
 
 /* Elementwise fmaf, exported so the numpy oracle's float32 FMA can be
@@ -518,8 +539,14 @@ int orc_moe_block(const orc_layer* L, const uint16_t* x, int T,
 #else
   (void)nthreads;
 #endif
+  uint16_t* xnorm = L->post_norm_w ? (uint16_t*)malloc((size_t)H * sizeof(uint16_t)) : NULL;
+  if (L->post_norm_w && !xnorm) return ORC_EINVAL;
   for (int t = 0; t < T; ++t) {
     const uint16_t* xt = x + (size_t)t * H;
+    if (xnorm) {
+      orc_rms_norm(xt, L->post_norm_w, H, L->norm_eps, xnorm);
+      xt = xnorm;
+    }
     int32_t idx[64];
     float scores[64];
     orc_route_token(L, xt, idx, scores, NULL);
@@ -539,7 +566,7 @@ int orc_moe_block(const orc_layer* L, const uint16_t* x, int T,
     float* act = (float*)malloc((size_t)n_units * maxI * sizeof(float));
     float* asum = (float*)malloc((size_t)n_units * maxI * sizeof(float));
     if (!xv || !xsum || !act || !asum) {
-      free(xv); free(xsum); free(act); free(asum);
+      free(xv); free(xsum); free(act); free(asum); free(xnorm);
       return ORC_EINVAL;
     }
     for (int h = 0; h < H; ++h) xv[h] = orc_bf16_to_f32(xt[h]);
@@ -581,6 +608,7 @@ int orc_moe_block(const orc_layer* L, const uint16_t* x, int T,
     free(act);
     free(asum);
   }
+  free(xnorm);
   return ORC_OK;
 }
 

@@ -57,7 +57,9 @@ def layer_to_dev(L, device="cuda"):
         else None,
         bank_to_dev(L.shared_gate_up, device, squeeze=True) if shared else None,
         bank_to_dev(L.shared_down, device, squeeze=True) if shared else None,
-        bits=L.gate_up.bits)
+        bits=L.gate_up.bits,
+        post_norm_w=None if L.post_norm_w is None else dev_bf16(L.post_norm_w, device),
+        norm_eps=L.norm_eps)
 
 
 def bank_from_dev(w, s, b, bits):
@@ -82,6 +84,9 @@ def layer_from_dev(lw):
 
     L = Layer(gu.cols, gu.rows // 2, E, lw.top_k, gate(lw.router_w), gu, dn,
               norm_topk_prob=lw.norm_topk_prob)
+    if lw.post_norm_w is not None:
+        L.post_norm_w = host_bf16(lw.post_norm_w)
+        L.norm_eps = lw.norm_eps
     if lw.shared_gate_up is not None:
         L.shared_gate_w = gate(lw.shared_gate_w)
         L.shared_gate_up = bank_from_dev(*lw.shared_gate_up, lw.bits)

@@ -304,6 +304,28 @@ def gate_logits(x_bits: np.ndarray, gate) -> np.ndarray:
     return router_logits(x_bits, gate)
 
 
+def rms_norm(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    """The decoder layer's post-attention RMSNorm in front of the block
+    (``mx.fast.rms_norm(x, w, eps)``; the checkpoints store the effective
+    weight): bf16 bits [T, H] -> bf16 bits [T, H].
+
+    This build's fixed order: s = sum x_k^2 in the router contract's order
+    (8-element chunks, lane l of 64 takes chunks l, l+64, ... from +0, then
+    the butterfly; the squares of bf16 values are exact in fp32), then in
+    fp32 with correct rounding ms = s / H, v = ms + eps, r = 1 / sqrt(v), and
+    per element n = bf16(x r), y = bf16(n w)."""
+    x_bits = np.asarray(x_bits, np.uint16)
+    T, H = x_bits.shape
+    s = np.empty(T, np.float32)
+    for t in range(T):
+        s[t] = router_logits(x_bits[t:t + 1], x_bits[t:t + 1])[0, 0]
+    ms = (s / np.float32(H)).astype(np.float32)
+    v = (ms + np.float32(eps)).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt(v)).astype(np.float32)
+    n = round_bf16(bf16_to_f32(x_bits) * r[:, None])
+    return f32_to_bf16(n * bf16_to_f32(np.asarray(w_bits, np.uint16))[None, :])
+
+
 def topk_rank(logits_bf16: np.ndarray, k: int) -> np.ndarray:
     """Indices [T, k] ordered by (logit desc, index asc)."""
     order = np.argsort(-logits_bf16, axis=-1, kind="stable")
@@ -390,13 +412,15 @@ class Layer:
     inter: int
     experts: int
     top_k: int
-    router_w: np.ndarray           # bf16 bits [E, H]
+    router_w: "np.ndarray | QWeight"   # bf16 bits [E, H], or an 8-bit bank [1, E, H]
     gate_up: QWeight               # [E, 2I, H], rows [up; gate]
     down: QWeight                  # [E, H, I]
-    shared_gate_w: np.ndarray | None = None   # bf16 bits [H]
+    shared_gate_w: "np.ndarray | QWeight | None" = None  # bf16 bits [H], or [1, 1, H]
     shared_gate_up: QWeight | None = None     # [1, 2Is, H]
     shared_down: QWeight | None = None        # [1, H, Is]
     norm_topk_prob: bool = True
+    post_norm_w: np.ndarray | None = None     # bf16 bits [H]: RMSNorm before the block
+    norm_eps: float = 1e-6
 
     @property
     def shared_inter(self):
@@ -453,7 +477,11 @@ def block_forward(layer: Layer, x_bits: np.ndarray, residual_bits=None,
                   mode: str = "contract", idx: np.ndarray | None = None):
     """Whole block.  x_bits [T, H] bf16 bits -> (out bf16 bits [T, H], idx,
     scores).  ``idx`` forces the routing (used to compare outputs when a
-    boundary tie leaves more than one valid selection)."""
+    boundary tie leaves more than one valid selection).  With
+    ``layer.post_norm_w`` the block's input is ``rms_norm(x)`` (the residual
+    stays what the caller passes)."""
+    if layer.post_norm_w is not None:
+        x_bits = rms_norm(x_bits, layer.post_norm_w, layer.norm_eps)
     r_idx, scores, logits = route(x_bits, layer.router_w, layer.top_k,
                                   layer.norm_topk_prob)
     if idx is None:
@@ -584,6 +612,7 @@ def c_oracle():
     lib.orc_qrouter_dot.argtypes = [P, ctypes.c_int, P]
     lib.orc_qrouter_dot.restype = ctypes.c_float
     lib.orc_fmaf_array.argtypes = [P, P, P, P, S]
+    lib.orc_rms_norm.argtypes = [P, P, ctypes.c_int, ctypes.c_float, P]
     lib.orc_moe_block.argtypes = [P, P, ctypes.c_int, P, P, P, P, ctypes.c_int]
     lib.orc_random_sequence.argtypes = [ctypes.c_uint64, S, P]
     lib.orc_random_sequence.restype = ctypes.c_uint32
@@ -707,7 +736,8 @@ class _CLayer(ctypes.Structure):
                 ("top_k", ctypes.c_int32), ("norm_topk_prob", ctypes.c_int32),
                 ("router_w", ctypes.c_void_p), ("shared_gate_w", ctypes.c_void_p),
                 ("gate_up", _CQW), ("down", _CQW), ("shared_gate_up", _CQW),
-                ("shared_down", _CQW), ("router_q", _CQW), ("shared_gate_q", _CQW)]
+                ("shared_down", _CQW), ("router_q", _CQW), ("shared_gate_q", _CQW),
+                ("post_norm_w", ctypes.c_void_p), ("norm_eps", ctypes.c_float)]
 
 
 def _cqw(q: QWeight | None, keep):
@@ -730,14 +760,17 @@ def c_block_forward(layer: Layer, x_bits: np.ndarray, residual_bits=None,
     router = None if rq is not None else np.ascontiguousarray(layer.router_w)
     sg = (None if layer.shared_gate_w is None or sgq is not None
           else np.ascontiguousarray(layer.shared_gate_w))
-    keep += [router, sg]
+    pnw = None if layer.post_norm_w is None else np.ascontiguousarray(layer.post_norm_w,
+                                                                        dtype=np.uint16)
+    keep += [router, sg, pnw]
     cl = _CLayer(layer.hidden, layer.inter, layer.shared_inter, layer.experts,
                  layer.top_k, int(layer.norm_topk_prob),
                  None if router is None else _p(router).value,
                  None if sg is None else _p(sg).value,
                  _cqw(layer.gate_up, keep), _cqw(layer.down, keep),
                  _cqw(layer.shared_gate_up, keep), _cqw(layer.shared_down, keep),
-                 _cqw(rq, keep), _cqw(sgq, keep))
+                 _cqw(rq, keep), _cqw(sgq, keep),
+                 None if layer.post_norm_w is None else _p(pnw).value, layer.norm_eps)
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     T = x.shape[0]
     out = np.zeros((T, layer.hidden), np.uint16)

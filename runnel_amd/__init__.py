@@ -8,11 +8,12 @@ Drop-in surfaces:
 The compute runs in runnel_amd/librmoe.so (hand-written HIP for gfx950).
 """
 
-from .moe import FusedQuantizedSwitchGLU, SparseMoeBlock, fuse_routed_gate_up
-from .switch_layers import (MLP, Linear, QuantizedLinear, QuantizedSwitchLinear,
+from .moe import FusedQuantizedSwitchGLU, PostAttentionMoE, SparseMoeBlock, fuse_routed_gate_up
+from .switch_layers import (MLP, Linear, QuantizedLinear, QuantizedSwitchLinear, RMSNorm,
                             SwiGLU, SwitchGLU)
 
 __all__ = [
-    "FusedQuantizedSwitchGLU", "SparseMoeBlock", "fuse_routed_gate_up",
-    "MLP", "Linear", "QuantizedLinear", "QuantizedSwitchLinear", "SwiGLU", "SwitchGLU",
+    "FusedQuantizedSwitchGLU", "PostAttentionMoE", "SparseMoeBlock", "fuse_routed_gate_up",
+    "MLP", "Linear", "QuantizedLinear", "QuantizedSwitchLinear", "RMSNorm", "SwiGLU",
+    "SwitchGLU",
 ]

@@ -21,7 +21,7 @@ RMOE_EWS = -4
 RMOE_EHIP = -5
 RMOE_ENULL = -6
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EXPORTED = (
     "rmoe_abi_version", "rmoe_last_error", "rmoe_status_string",
@@ -30,7 +30,7 @@ EXPORTED = (
     "rmoe_moe_block", "rmoe_quantize", "rmoe_dequantize", "rmoe_stream_read",
     "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes", "rmoe_chain_table_pack",
     "rmoe_moe_chain", "rmoe_workspace_status_offset", "rmoe_router_q",
-    "rmoe_switch_combine", "rmoe_switch_combine_workspace_bytes",
+    "rmoe_switch_combine", "rmoe_switch_combine_workspace_bytes", "rmoe_rms_norm",
 )
 
 
@@ -62,6 +62,7 @@ class Layer(ctypes.Structure):
         ("gate_up", QWeight), ("down", QWeight),
         ("shared_gate_up", QWeight), ("shared_down", QWeight),
         ("router_q", QWeight), ("shared_gate_q", QWeight),
+        ("post_norm_w", ctypes.c_void_p), ("norm_eps", ctypes.c_float),
     ]
 
 
@@ -101,6 +102,7 @@ def load() -> ctypes.CDLL:
         lib.rmoe_switch_workspace_bytes.argtypes = [QP, QP, I32, I32]
         lib.rmoe_router.argtypes = [P, I32, I32, I32, I32, P, I32, P, P, P, SZ, P]
         lib.rmoe_router_q.argtypes = [QP, I32, I32, P, I32, P, P, P, SZ, P]
+        lib.rmoe_rms_norm.argtypes = [P, P, I32, I32, ctypes.c_float, P, P]
         lib.rmoe_router_workspace_bytes.restype = SZ
         lib.rmoe_router_workspace_bytes.argtypes = [I32, I32, I32]
         lib.rmoe_switch_glu.argtypes = [QP, QP, P, I32, P, I32, P, P, SZ, P]

@@ -290,6 +290,25 @@ def load_moe_block(root_or_store, layer: int, device="cuda", config: dict | None
     return blk
 
 
+def load_decoder_moe(root_or_store, layer: int, device="cuda", config: dict | None = None):
+    """The MoE half of decoder layer `layer`: its ``post_attention_layernorm``
+    (weight and the config's ``rms_norm_eps``) in front of the block, as a
+    ``PostAttentionMoE`` computing ``h + mlp(norm(h))``."""
+    from .moe import PostAttentionMoE
+    from .switch_layers import RMSNorm
+    store = (root_or_store if isinstance(root_or_store, SafeTensorStore)
+             else SafeTensorStore(root_or_store))
+    cfg = _load_config(store, config)
+    text = cfg.get("text_config", cfg)
+    H = int(text["hidden_size"])
+    name = _layer_prefix(store, layer)[:-len(".mlp")] + ".post_attention_layernorm.weight"
+    info = store.info(name)
+    if info.shape != (H,) or info.dtype != "BF16":
+        raise ValueError(f"{name}: expected BF16 [{H}], found {info.dtype} {list(info.shape)}")
+    norm = RMSNorm(H, float(text.get("rms_norm_eps", 1e-6)), weight=store.tensor(name, device))
+    return PostAttentionMoE(norm, load_moe_block(store, layer, device, cfg))
+
+
 # ------------------------------------------------------------------ RNLMOE01
 
 MOE_MAGIC = b"RNLMOE01"

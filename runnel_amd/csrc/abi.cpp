@@ -154,6 +154,12 @@ int check_layer(const rmoe_layer* L) {
     return rc;
   if (L->shared_gate_w && !aligned(L->shared_gate_w, 16))
     return fail(RMOE_EALIGN, "shared_gate_w must be 16-byte aligned");
+  if (L->post_norm_w) {
+    if (!aligned(L->post_norm_w, 16))
+      return fail(RMOE_EALIGN, "post_norm_w must be 16-byte aligned");
+    if (!(L->norm_eps >= 0.0f) || L->norm_eps > 1.0f)
+      return fail(RMOE_EINVAL, "norm_eps must be in [0, 1] (got %g)", (double)L->norm_eps);
+  }
   return RMOE_OK;
 }
 
@@ -170,6 +176,7 @@ struct Layout {
   // expert-sorted (prefill) path
   size_t rows, offs, tile_offs, tile_desc, hist, act16, y16, wnorm;
   size_t split;  // bf16 planes of a quantized gate (matrix-core router)
+  size_t xn;     // RMSNorm of x [T, H] bf16 (layers with post_norm_w)
 };
 
 // Calls that route at least kPrefillMinRows (token, slot) rows take the
@@ -234,7 +241,12 @@ Layout block_layout(const rmoe_layer* L, int T) {
   const bool sorted = prefill_path(T, L->top_k, L->experts, L->hidden, L->inter);
   const bool split = sorted && router_quantized(L) &&
                      rmoe::router_mfma_eligible(L->experts, L->hidden);
-  return layout(T, L->experts, L->top_k, L->inter, L->hidden, sorted, true, split);
+  Layout l = layout(T, L->experts, L->top_k, L->inter, L->hidden, sorted, true, split);
+  if (L->post_norm_w) {
+    l.xn = l.total;
+    l.total = align_up(l.total + (size_t)T * L->hidden * sizeof(uint16_t));
+  }
+  return l;
 }
 
 rmoe::PrefillArgs prefill_args(const Layout& l, void* ws, int T, int H, int I, int E, int K,
@@ -319,7 +331,9 @@ bool fused_eligible(const rmoe_layer* L, int* grid) {
   if (L->hidden != rmoe::kFusedH || L->inter != rmoe::kFusedI) return false;
   if (units > rmoe::kMaxFusedUnits || L->experts > rmoe::kFusedMaxExperts) return false;
   int g = 0;
-  if (rmoe::fused_grid(L->gate_up.bits, router_quantized(L), &g) != hipSuccess) return false;
+  if (rmoe::fused_grid(L->gate_up.bits, router_quantized(L), L->post_norm_w != nullptr, &g) !=
+      hipSuccess)
+    return false;
   const int waves = g * (rmoe::kFusedThreads / 64);
   // the router rows are computed once per XCD by its g / 8 workgroups
   if (g % 8 != 0 || g < L->experts) return false;
@@ -342,6 +356,8 @@ rmoe::FusedLayer fused_layer(const rmoe_layer* L) {
   f.sdn = qw(L->shared_down);
   f.rq = qw(L->router_q);
   f.sgq = qw(L->shared_gate_q);
+  f.norm_w = L->post_norm_w;
+  f.norm_eps = L->norm_eps;
   return f;
 }
 
@@ -354,6 +370,7 @@ rmoe::FusedArgs fused_args(const rmoe_layer* L, const uint16_t* x, uint16_t* out
   f.norm = L->norm_topk_prob != 0;
   f.has_shared = L->shared_gate_up.w != nullptr;
   f.rq8 = router_quantized(L);
+  f.rms_norm = L->post_norm_w != nullptr;
   f.layer0 = fused_layer(L);
   f.table = nullptr;
   f.x = x;
@@ -541,6 +558,24 @@ int rmoe_router(const uint16_t* router_w, int32_t experts, int32_t hidden,
   return ok();
 }
 
+int rmoe_rms_norm(const uint16_t* x, const uint16_t* weight, int32_t tokens, int32_t hidden,
+                  float eps, uint16_t* out, void* stream) {
+  int rc;
+  if ((rc = check_tokens(tokens))) return rc;
+  if (hidden < 8 || hidden % 8)
+    return fail(RMOE_EINVAL, "hidden must be a positive multiple of 8 (got %d)", hidden);
+  if (!(eps >= 0.0f) || eps > 1.0f)
+    return fail(RMOE_EINVAL, "eps must be in [0, 1] (got %g)", (double)eps);
+  if (tokens == 0) return ok();
+  if (!x || !weight || !out) return fail(RMOE_ENULL, "x, weight and out are required");
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, 16))
+    return fail(RMOE_EALIGN, "x, weight and out must be 16-byte aligned");
+  const hipError_t e = rmoe::launch_rmsnorm(x, weight, tokens, hidden, eps, out,
+                                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+  return ok();
+}
+
 int rmoe_router_q(const rmoe_qweight* router, int32_t top_k, int32_t norm_topk_prob,
                   const uint16_t* x, int32_t tokens, int32_t* indices, float* scores,
                   void* ws, size_t ws_bytes, void* stream) {
@@ -608,12 +643,19 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
     if (e != hipSuccess) return hip_fail(e, "fused decode launch");
     return ok();
   }
+  hipError_t e;
+  if (L->post_norm_w) {
+    // the block's input is RMSNorm(x); the residual stays the caller's
+    uint16_t* xn = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + lay.xn);
+    e = rmoe::launch_rmsnorm(x, L->post_norm_w, tokens, L->hidden, L->norm_eps, xn, s);
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+    x = xn;
+  }
   rmoe::DecodeArgs a = decode_args(L, x, tokens, ws);
   a.out = out;
   a.residual = residual;
   a.idx_out = indices_out;
   a.scores_out = scores_out;
-  hipError_t e;
   if (lay.rows && rmoe::router_mfma_eligible(L->experts, L->hidden))
     e = rmoe::launch_router_mfma(
         a, reinterpret_cast<float*>(static_cast<char*>(ws) + lay.wnorm),
@@ -747,7 +789,8 @@ int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers, void* host
         (b.shared_gate_up.w == nullptr) != (a.shared_gate_up.w == nullptr) ||
         (b.shared_gate_w == nullptr) != (a.shared_gate_w == nullptr) ||
         (b.router_q.w == nullptr) != (a.router_q.w == nullptr) ||
-        (b.shared_gate_q.w == nullptr) != (a.shared_gate_q.w == nullptr))
+        (b.shared_gate_q.w == nullptr) != (a.shared_gate_q.w == nullptr) ||
+        (b.post_norm_w == nullptr) != (a.post_norm_w == nullptr))
       return fail(RMOE_EINVAL, "layer %d differs in shape or format from layer 0", i);
   }
   for (int i = 0; i < n_layers; ++i) {

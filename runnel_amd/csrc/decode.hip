@@ -578,6 +578,47 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
   finish_route<P>(p, t, out, sg_logit, s_topk[wave]);
 }
 
+// ----------------------------------------------------------------- RMSNorm
+// out[t] = bf16(bf16(x[t] r) w), r = 1 / sqrt(sum(x^2) / H + eps): the sum in
+// the router contract's order (8-value chunks, lane l takes chunks l, l+64,
+// ..., then the butterfly), ms, v, r correctly rounded in fp32 (the library is
+// built with correctly rounded fp32 division and square root).  One wave
+// per token.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, const uint16_t* w,
+                                                      int T, int H, float eps, uint16_t* out) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const uint16_t* xt = x + (size_t)t * H;
+  const int chunks = H >> 3;
+  float acc = 0.0f;
+  for (int c = lane; c < chunks; c += 64) {
+    const uint4 v = load16(xt + c * 8);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), acc);
+      acc = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), acc);
+    }
+  }
+  const float ms = wave_sum(acc) / (float)H;
+  const float r = 1.0f / sqrtf(ms + eps);
+  for (int c = lane; c < chunks; c += 64) {
+    const uint4 v = load16(xt + c * 8);
+    const uint4 g = load16(w + c * 8);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t gg[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = round_bf16(bf16_lo(vv[i]) * r) * bf16_lo(gg[i]);
+      const float hi = round_bf16(bf16_hi(vv[i]) * r) * bf16_hi(gg[i]);
+      o[i] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + (size_t)t * H + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // ----------------------------------------------------------------- gate/up
 template <int BITS>
 struct Packing {
@@ -901,6 +942,13 @@ hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split
     hipLaunchKernelGGL(router_select_kernel<0>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   }
+  RMOE_CHECK_LAUNCH();
+  return hipSuccess;
+}
+
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, float eps,
+                          uint16_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, T, H, eps, out);
   RMOE_CHECK_LAUNCH();
   return hipSuccess;
 }

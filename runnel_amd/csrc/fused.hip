@@ -377,7 +377,7 @@ __device__ __forceinline__ void issue_shared_pairs(const FusedLayer& L, bool has
   issue_fence();
 }
 
-template <int BITS, int RQ>
+template <int BITS, int RQ, bool NORM>
 __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs p) {
   using S = Shape<BITS>;
   constexpr int H = S::H;
@@ -411,7 +411,9 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   const int pw = wg + G * wave;
   FusedScratch* sc = p.scratch;
 
-  __shared__ float s_x[H];
+  __shared__ float s_x[H];                 // the layer input (and residual)
+  __shared__ float s_n[NORM ? H : 4];      // its RMSNorm, the block's input
+  float* const s_in = NORM ? s_n : s_x;
   __shared__ float s_act[NU * I];
   __shared__ int s_idx[NU];
   __shared__ float s_coef[NU];
@@ -427,8 +429,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   DownRegs<S::DN_WPL> dr[NU];      // slot NU-1: the shared unit
   uint32_t dpw0 = 0, dpw1 = 0;
   GateRow<RQ> rw, sw;  // router row; shared gate row (wave kPollWave)
+  uint2 nw = make_uint2(0, 0);  // RMSNorm weights of values 4 t .. 4 t + 3
   {
     const FusedLayer L0 = p.table ? p.table[0] : p.layer0;
+    // the norm weights first: the oldest load is the first one waited for
+    if constexpr (NORM) nw = *reinterpret_cast<const uint2*>(L0.norm_w + 4 * threadIdx.x);
     issue_router_and_shared_down<BITS, RQ>(L0, row, E, p.has_shared, h, lane0,
                                            wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
     issue_shared_pairs<BITS, CPL, NP>(L0, p.has_shared, K, pw, n_waves, n_pairs, lane0, pr);
@@ -465,9 +470,38 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     }
     __syncthreads();
 
+    // ---- RMSNorm: every wave sums the squares in the contract's order (8
+    // values per chunk, chunks lane + 64 i, then the butterfly) and gets the
+    // same r; each thread then writes its 4 normalised values.
+    if constexpr (NORM) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < H / 512; ++i) {
+        const float4 a = *reinterpret_cast<const float4*>(s_x + (lane + 64 * i) * 8);
+        const float4 b = *reinterpret_cast<const float4*>(s_x + (lane + 64 * i) * 8 + 4);
+        acc = fmaf(a.x, a.x, acc);
+        acc = fmaf(a.y, a.y, acc);
+        acc = fmaf(a.z, a.z, acc);
+        acc = fmaf(a.w, a.w, acc);
+        acc = fmaf(b.x, b.x, acc);
+        acc = fmaf(b.y, b.y, acc);
+        acc = fmaf(b.z, b.z, acc);
+        acc = fmaf(b.w, b.w, acc);
+      }
+      const float ms = wave_sum(acc) / (float)H;
+      const float r = 1.0f / sqrtf(ms + L.norm_eps);
+      const float4 v = *reinterpret_cast<const float4*>(s_x + 4 * threadIdx.x);
+      *reinterpret_cast<float4*>(s_n + 4 * threadIdx.x) =
+          make_float4(round_bf16(round_bf16(v.x * r) * bf16_lo(nw.x)),
+                      round_bf16(round_bf16(v.y * r) * bf16_hi(nw.x)),
+                      round_bf16(round_bf16(v.z * r) * bf16_lo(nw.y)),
+                      round_bf16(round_bf16(v.w * r) * bf16_hi(nw.y)));
+      __syncthreads();
+    }
+
     // ---- R: this wave's router row.
     if (row < E) {
-      const float acc = wave_sum(gate_partial(rw, s_x, lane));
+      const float acc = wave_sum(gate_partial(rw, s_in, lane));
       if (lane == 0)
         __builtin_amdgcn_raw_buffer_store_b32(
             tagged(f32_to_bf16(acc), tag_logit),
@@ -479,7 +513,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     if (wave == kPollWave) {
       // the shared gate's logit, computed here (its row is not handed over)
       uint32_t wsg = 0;
-      if (sg_row) wsg = f32_to_bf16(wave_sum(gate_partial(sw, s_x, lane))) << 16;
+      if (sg_row) wsg = f32_to_bf16(wave_sum(gate_partial(sw, s_in, lane))) << 16;
       // lane l holds experts 4 l .. 4 l + 3 (one 16-byte load from the L2)
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           sc->logits[xcd], (short)0, E * 4, 0x00020000);
@@ -592,7 +626,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       xs[i] = 0.0f;
 #pragma unroll
       for (int v = 0; v < VPC; v += 4) {
-        const float4 f = *reinterpret_cast<const float4*>(s_x + ch * VPC + v);
+        const float4 f = *reinterpret_cast<const float4*>(s_in + ch * VPC + v);
         xv[i][v] = f.x;
         xv[i][v + 1] = f.y;
         xv[i][v + 2] = f.z;
@@ -713,6 +747,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     // extra loads (shared gate row, shared pairs) are back by then.
     if (!last) {
       const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
+      if constexpr (NORM) nw = *reinterpret_cast<const uint2*>(Ln.norm_w + 4 * threadIdx.x);
       issue_router_and_shared_down<BITS, RQ>(Ln, row, E, p.has_shared, h, lane,
                                              wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
       issue_shared_pairs<BITS, CPL, NP>(Ln, p.has_shared, K, pw, n_waves, n_pairs, lane, pr);
@@ -727,20 +762,24 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 }
 
 namespace {
-const void* fused_fn(int bits, int rq8) {
-  if (bits == 8)
-    return rq8 ? (const void*)fused_decode_kernel<8, 1> : (const void*)fused_decode_kernel<8, 0>;
-  return rq8 ? (const void*)fused_decode_kernel<4, 1> : (const void*)fused_decode_kernel<4, 0>;
+template <int BITS, int RQ>
+const void* fused_fn_n(int norm) {
+  return norm ? (const void*)fused_decode_kernel<BITS, RQ, true>
+              : (const void*)fused_decode_kernel<BITS, RQ, false>;
+}
+const void* fused_fn(int bits, int rq8, int norm) {
+  if (bits == 8) return rq8 ? fused_fn_n<8, 1>(norm) : fused_fn_n<8, 0>(norm);
+  return rq8 ? fused_fn_n<4, 1>(norm) : fused_fn_n<4, 0>(norm);
 }
 }  // namespace
 
-hipError_t fused_grid(int bits, int rq8, int* grid) {
+hipError_t fused_grid(int bits, int rq8, int norm, int* grid) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   // Occupancy does not change for a device: cache it (grid + 1, 0 = unknown).
-  static int cache[64][4];
-  const int slot = (bits == 8 ? 0 : 2) + (rq8 ? 1 : 0);
+  static int cache[64][8];
+  const int slot = (bits == 8 ? 0 : 4) + (rq8 ? 2 : 0) + (norm ? 1 : 0);
   if (dev >= 0 && dev < 64) {
     const int c = __atomic_load_n(&cache[dev][slot], __ATOMIC_RELAXED);
     if (c > 0) {
@@ -752,7 +791,8 @@ hipError_t fused_grid(int bits, int rq8, int* grid) {
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   int per_cu = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_fn(bits, rq8), kThreads, 0);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_fn(bits, rq8, norm),
+                                                   kThreads, 0);
   if (e != hipSuccess) return e;
   *grid = per_cu >= 1 ? (cus < kFusedMaxGrid ? cus : kFusedMaxGrid) : 0;
   if (dev >= 0 && dev < 64) __atomic_store_n(&cache[dev][slot], *grid + 1, __ATOMIC_RELAXED);
@@ -762,7 +802,7 @@ hipError_t fused_grid(int bits, int rq8, int* grid) {
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s) {
   FusedArgs args = a;
   void* kargs[] = {&args};
-  const void* fn = fused_fn(bits, a.rq8);
+  const void* fn = fused_fn(bits, a.rq8, a.rms_norm);
   // A cooperative launch guarantees every workgroup is resident.  Under
   // stream capture a plain launch of the same one-workgroup-per-CU grid is
   // recorded instead (every workgroup fits at once on an otherwise idle

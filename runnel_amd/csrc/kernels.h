@@ -71,6 +71,8 @@ struct FusedLayer {
   const uint16_t* sgate_w;
   QW gu, dn, sgu, sdn;
   QW rq, sgq;                 // 8-bit gates when the call's rq8 is set
+  const uint16_t* norm_w;     // RMSNorm weights [H] when the call's norm is set
+  float norm_eps;
 };
 
 // Device scratch of the fused kernel: lives at a fixed workspace offset so
@@ -88,6 +90,7 @@ struct FusedScratch {
 struct FusedArgs {
   int n_layers, E, K, norm, has_shared;
   int rq8;                    // gates are 8-bit MLX-affine (every layer)
+  int rms_norm;               // RMSNorm of the layer input (every layer)
   int residual_mode;          // 0 none, 1 the layer input, 2 `residual`
   FusedLayer layer0;          // used when table == nullptr
   const FusedLayer* table;    // device array of n_layers descriptors
@@ -99,10 +102,13 @@ struct FusedArgs {
   float* scores_out;
 };
 
-hipError_t fused_grid(int bits, int rq8, int* grid);
+hipError_t fused_grid(int bits, int rq8, int rms_norm, int* grid);
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s);
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s);
+// RMSNorm of T rows of H bf16 values (H a multiple of 8; x, w, out 16-byte aligned).
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, float eps,
+                          uint16_t* out, hipStream_t s);
 // Many-token router on the matrix cores with exact selection (prefill).
 bool router_mfma_eligible(int E, int H);
 // wnorm: [E] floats; split: [2, E, H] bf16 (quantized gates only)

@@ -20,7 +20,7 @@ import torch
 from torch import nn
 
 from . import native
-from .switch_layers import (MLP, Linear, QuantizedLinear, QuantizedSwitchLinear,
+from .switch_layers import (MLP, Linear, QuantizedLinear, QuantizedSwitchLinear, RMSNorm,
                             SwiGLU, SwitchGLU, swiglu)
 
 BF16 = torch.bfloat16
@@ -121,7 +121,7 @@ def fuse_routed_gate_up(model) -> int:
         fused = FusedQuantizedSwitchGLU(old)
         layer.mlp.switch_mlp = fused
         if isinstance(layer.mlp, SparseMoeBlock):
-            layer.mlp._handle = None
+            layer.mlp._handles = {}
         count += 1
         del old, fused
         gc.collect()
@@ -173,14 +173,16 @@ class SparseMoeBlock(nn.Module):
         else:
             self.shared_expert = None
             self.shared_expert_gate = None
-        self._handle = None
+        self._handles = {}
 
     # ------------------------------------------------------------ fast path
-    def layer_handle(self) -> native.LayerHandle | None:
-        """rmoe_layer for the fused three-kernel path, or None when the
-        modules are not in the packed / SwiGLU / affine form it needs."""
-        if self._handle is not None:
-            return self._handle
+    def layer_handle(self, post_norm: RMSNorm | None = None) -> native.LayerHandle | None:
+        """rmoe_layer for the fused path (with `post_norm` in front of the
+        block when given), or None when the modules are not in the packed /
+        SwiGLU / affine form it needs.  Cached per norm module."""
+        key = None if post_norm is None else id(post_norm)
+        if key in self._handles:
+            return self._handles[key][0]
         sm = self.switch_mlp
         if not isinstance(sm, FusedQuantizedSwitchGLU) or not sm._fast_path():
             return None
@@ -204,14 +206,17 @@ class SparseMoeBlock(nn.Module):
             if sgate is None or type(self.shared_expert_gate) is not type(self.gate):
                 return None
         dp = sm.down_proj
-        self._handle = native.make_layer(
+        h = native.make_layer(
             router, (sm.weight, sm.scales, sm.biases),
             (dp.weight, dp.scales, dp.biases), self.top_k, self.norm_topk_prob,
             shared_gate_w=sgate,
             shared_gate_up=None if shared is None else shared[0],
             shared_down=None if shared is None else shared[1],
-            bits=sm.bits, group_size=sm.group_size)
-        return self._handle
+            bits=sm.bits, group_size=sm.group_size,
+            post_norm_w=None if post_norm is None else post_norm.weight,
+            norm_eps=1e-6 if post_norm is None else post_norm.eps)
+        self._handles[key] = (h, post_norm)   # the norm module is kept alive with its key
+        return h
 
     def __call__(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
         D = x.shape[-1]
@@ -242,3 +247,28 @@ class SparseMoeBlock(nn.Module):
         if residual is not None:
             out = (residual.reshape(-1, D).float() + out.float()).to(BF16)
         return out.reshape(*lead, D)
+
+
+class PostAttentionMoE(nn.Module):
+    """The MoE half of a decoder layer: ``h + mlp(post_attention_layernorm(h))``
+    (the residual/norm sequence of docs/architecture.md:31-37).  With the
+    block's fast path this is one rmoe_moe_block call (RMSNorm, router,
+    experts, combine and residual add); `native.Chain` of the same handles
+    runs a stack of layers in one launch."""
+
+    def __init__(self, post_attention_layernorm: RMSNorm, mlp: SparseMoeBlock):
+        super().__init__()
+        self.post_attention_layernorm = post_attention_layernorm
+        self.mlp = mlp
+
+    def layer_handle(self) -> native.LayerHandle | None:
+        return self.mlp.layer_handle(self.post_attention_layernorm)
+
+    def __call__(self, h: torch.Tensor) -> torch.Tensor:
+        D = h.shape[-1]
+        lead = h.shape[:-1]
+        lh = self.layer_handle()
+        h2 = h.reshape(-1, D)
+        if lh is not None:
+            return native.moe_block(lh, h2, residual=h2).reshape(*lead, D)
+        return self.mlp(self.post_attention_layernorm(h2), residual=h2).reshape(*lead, D)

@@ -194,12 +194,14 @@ def _gate(g, rows: int | None, name: str):
 
 def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
                shared_gate_w=None, shared_gate_up=None, shared_down=None,
-               bits: int = 8, group_size: int = 64) -> LayerHandle:
+               bits: int = 8, group_size: int = 64, post_norm_w=None,
+               norm_eps: float = 1e-6) -> LayerHandle:
     """router_w bf16 [E, H], or the (weight, scales, biases) triple of an
     8-bit group-64 quantized gate (QuantizedLinear); shared_gate_w likewise
     (bf16 [H] or a one-row triple, in the router's format); gate_up / down /
     shared_* are (weight, scales, biases) triples of packed banks; shared
-    banks may omit the expert axis."""
+    banks may omit the expert axis.  post_norm_w (bf16 [H]) puts the
+    decoder's post-attention RMSNorm in front of the block."""
     gu = qweight_struct(*gate_up, bits, group_size)
     dn = qweight_struct(*down, bits, group_size)
     router_w, rq, rkeep = _gate(router_w, None, "router gate")
@@ -227,8 +229,14 @@ def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
         E, H = router_w.shape
     else:
         E, H = rq.rows, rq.cols
+    if post_norm_w is not None:
+        post_norm_w = post_norm_w.reshape(-1).contiguous()
+        if post_norm_w.dtype != BF16 or post_norm_w.numel() != H:
+            raise ValueError(f"post_norm_w must be bfloat16 [{H}]")
+        keep.append(post_norm_w)
     s = _lib.Layer(H, gu.rows // 2, shared_inter, E, top_k, int(bool(norm_topk_prob)),
-                   _lib.ptr(router_w), _lib.ptr(shared_gate_w), gu, dn, sgu, sdn, rq, sgq)
+                   _lib.ptr(router_w), _lib.ptr(shared_gate_w), gu, dn, sgu, sdn, rq, sgq,
+                   _lib.ptr(post_norm_w), float(norm_eps))
     h = LayerHandle(s, tuple(keep))
     h.validate()
     return h
@@ -331,6 +339,24 @@ def router(router_w, x: torch.Tensor, top_k: int, norm_topk_prob: bool = True):
                                    x.data_ptr(), T, idx.data_ptr(), scores.data_ptr(),
                                    ws.data_ptr(), ws.numel(), _lib.stream_handle(x.device)))
     return idx, scores
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm of the rows of x bf16 [..., H] with weight bf16 [H]
+    (mx.fast.rms_norm) -> bf16, in the library's fixed order."""
+    lib = _lib.load()
+    _require_cuda(x, weight)
+    if x.dtype != BF16 or weight.dtype != BF16:
+        raise ValueError("rms_norm takes bfloat16 x and weight")
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H).contiguous()
+    w = weight.reshape(-1).contiguous()
+    if w.numel() != H:
+        raise ValueError(f"weight must have {H} values (got {w.numel()})")
+    out = torch.empty_like(x2)
+    _lib.check(lib.rmoe_rms_norm(x2.data_ptr(), w.data_ptr(), x2.shape[0], H, float(eps),
+                                 out.data_ptr(), _lib.stream_handle(x.device)))
+    return out.reshape(x.shape)
 
 
 def quantize(w: torch.Tensor, bits: int, group_size: int = 64):

@@ -56,6 +56,21 @@ def native_linear(x2d: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.matmul(x2d.to(BF16), w.t().contiguous()).to(BF16)
 
 
+class RMSNorm(_Params):
+    """mlx ``nn.RMSNorm``: ``weight`` bf16 [dims], ``eps``; the decoder's
+    ``post_attention_layernorm`` in front of the MoE block."""
+
+    def __init__(self, dims: int, eps: float = 1e-6, weight=None, device=None):
+        super().__init__()
+        if weight is None:
+            weight = torch.ones(dims, dtype=BF16, device=device)
+        self.register_buffer("weight", weight.to(BF16).contiguous())
+        self.eps = float(eps)
+
+    def __call__(self, x):
+        return native.rms_norm(x, self.weight, self.eps)
+
+
 class QuantizedLinear(_Params):
     """MLX-affine quantized linear: weight int32 [out, in*bits/32], scales /
     biases bf16 [out, in/group]."""

@@ -30,11 +30,14 @@ class LayerWeights:
     bits: int
     top_k: int
     norm_topk_prob: bool = True
+    post_norm_w: torch.Tensor | None = None   # bf16 [H]: RMSNorm before the block
+    norm_eps: float = 1e-6
 
     def handle(self) -> native.LayerHandle:
         return native.make_layer(self.router_w, self.gate_up, self.down, self.top_k,
                                  self.norm_topk_prob, self.shared_gate_w,
-                                 self.shared_gate_up, self.shared_down, self.bits)
+                                 self.shared_gate_up, self.shared_down, self.bits,
+                                 post_norm_w=self.post_norm_w, norm_eps=self.norm_eps)
 
     def tensors(self):
         def flat(g):
@@ -42,6 +45,8 @@ class LayerWeights:
         ts = [*flat(self.router_w), *self.gate_up, *self.down]
         if self.shared_gate_up is not None:
             ts += [*flat(self.shared_gate_w), *self.shared_gate_up, *self.shared_down]
+        if self.post_norm_w is not None:
+            ts.append(self.post_norm_w)
         return ts
 
     def nbytes(self) -> int:
@@ -69,7 +74,7 @@ def _quantized_bank(gen, experts, rows, cols, bits, std, device, chunk_rows=1 <<
 
 def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8, bits=8,
                shared=True, std=0.02, router_std=0.02, device="cuda",
-               shared_inter=None, gate_bits=None) -> LayerWeights:
+               shared_inter=None, gate_bits=None, post_norm=False) -> LayerWeights:
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     shared_inter = inter if shared_inter is None else shared_inter
@@ -92,7 +97,11 @@ def make_layer(seed: int, hidden=2048, inter=512, experts=256, top_k=8, bits=8,
         sg = gate((hidden,))
         sgu = _quantized_bank(gen, 1, 2 * shared_inter, hidden, bits, std, device)
         sdn = _quantized_bank(gen, 1, hidden, shared_inter, bits, std, device)
-    return LayerWeights(router, gu, dn, sg, sgu, sdn, bits, top_k)
+    lw = LayerWeights(router, gu, dn, sg, sgu, sdn, bits, top_k)
+    if post_norm:
+        # RMSNorm weights around 1 (uniform in [0.5, 1.5])
+        lw.post_norm_w = (torch.rand((hidden,), generator=gen, device=device) + 0.5).to(BF16)
+    return lw
 
 
 def make_x(seed: int, tokens: int, hidden: int, device="cuda") -> torch.Tensor:

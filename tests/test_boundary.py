@@ -130,6 +130,34 @@ def test_validate_quantized_gates():
     assert lib.rmoe_validate_layer(ctypes.byref(no_shared)) == _lib.RMOE_EINVAL
 
 
+def test_post_norm_validation_and_rms_norm_arguments():
+    lib = _lib.load()
+    L = _layer()
+    L.post_norm_w = FAKE
+    L.norm_eps = 1e-6
+    assert lib.rmoe_validate_layer(ctypes.byref(L)) == _lib.RMOE_OK
+    L.post_norm_w = FAKE + 2
+    assert lib.rmoe_validate_layer(ctypes.byref(L)) == _lib.RMOE_EALIGN
+    L.post_norm_w = FAKE
+    for bad in (-1e-6, float("nan"), 2.0):
+        L.norm_eps = bad
+        assert lib.rmoe_validate_layer(ctypes.byref(L)) == _lib.RMOE_EINVAL
+    L.norm_eps = 1e-5
+    plain = lib.rmoe_workspace_bytes(ctypes.byref(_layer()), 5)
+    assert lib.rmoe_workspace_bytes(ctypes.byref(L), 5) >= plain + 5 * 256 * 2
+    assert lib.rmoe_rms_norm(FAKE, FAKE, 3, 100, 1e-6, FAKE, None) == _lib.RMOE_EINVAL
+    assert lib.rmoe_rms_norm(FAKE, FAKE, 3, 128, -1.0, FAKE, None) == _lib.RMOE_EINVAL
+    assert lib.rmoe_rms_norm(FAKE + 2, FAKE, 3, 128, 1e-6, FAKE, None) == _lib.RMOE_EALIGN
+    assert lib.rmoe_rms_norm(None, FAKE, 3, 128, 1e-6, FAKE, None) == _lib.RMOE_ENULL
+    assert lib.rmoe_rms_norm(None, None, 0, 128, 1e-6, None, None) == _lib.RMOE_OK
+    normed = _layer(H=2048, I=512, E=256, K=8)
+    normed.post_norm_w = FAKE
+    layers = (_lib.Layer * 2)(normed, _layer(H=2048, I=512, E=256, K=8))
+    buf = (ctypes.c_uint8 * lib.rmoe_chain_table_bytes(2))()
+    assert lib.rmoe_chain_table_pack(layers, 2, ctypes.addressof(buf)) == _lib.RMOE_EINVAL
+    assert b"layer 1 differs" in lib.rmoe_last_error()
+
+
 def test_quantized_router_rejects_before_launch():
     lib = _lib.load()
     r = _qw(8, 1, 16, 256)

@@ -187,6 +187,27 @@ def test_load_moe_block_from_checkpoint(tmp_path, bits, router_bits):
     assert (h.struct.router_q.w is not None) == (router_bits is not None)
 
 
+def test_load_decoder_moe_reads_the_post_attention_norm(tmp_path):
+    from runnel_amd import PostAttentionMoE
+    L = M.make_layer(5, hidden=256, inter=128, experts=8, top_k=2, bits=8)
+    nw = M.f32_to_bf16(np.linspace(0.5, 1.5, 256).astype(np.float32))
+    write_checkpoint(tmp_path, L, layer=1,
+                     extra={"language_model.model.layers.1.post_attention_layernorm.weight":
+                            ("BF16", nw)})
+    cfg = json.loads((tmp_path / "config.json").read_text())
+    cfg["text_config"]["rms_norm_eps"] = 1e-5
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    step = C.load_decoder_moe(tmp_path, 1, device="cpu")
+    assert isinstance(step, PostAttentionMoE)
+    norm = step.post_attention_layernorm
+    assert norm.eps == pytest.approx(1e-5)
+    assert np.array_equal(norm.weight.view(torch.int16).numpy().view(np.uint16), nw)
+    h = step.layer_handle()
+    assert h.struct.post_norm_w == norm.weight.data_ptr()
+    assert h.struct.norm_eps == pytest.approx(1e-5)
+    assert step.mlp.layer_handle().struct.post_norm_w is None   # the plain block's handle
+
+
 def test_load_moe_block_reports_missing_and_misshaped_tensors(tmp_path):
     L = M.make_layer(4, hidden=256, inter=128, experts=8, top_k=2, bits=8)
     write_checkpoint(tmp_path / "a", L)

@@ -396,3 +396,64 @@ def test_quantized_gate_routes_like_its_dequantised_bf16_gate_mostly():
     ib, _, _ = M.route(x, wf, 8)
     same = np.mean([len(set(a) & set(b)) / 8 for a, b in zip(iq, ib)])
     assert same > 0.9
+
+
+# ---------------------------------------------------------------- RMSNorm
+
+
+def _c_rms_norm(x, w, eps):
+    lib = M.c_oracle()
+    out = np.zeros_like(x)
+    for t in range(x.shape[0]):
+        row = np.ascontiguousarray(x[t])
+        o = np.zeros(x.shape[1], np.uint16)
+        lib.orc_rms_norm(M._p(row), M._p(np.ascontiguousarray(w)), x.shape[1], eps, M._p(o))
+        out[t] = o
+    return out
+
+
+@pytest.mark.parametrize("H", [2048, 512, 320])
+def test_rms_norm_equals_c_restatement(H):
+    rng = np.random.default_rng(H)
+    x = M.f32_to_bf16((rng.standard_normal((5, H)) * 3).astype(np.float32))
+    w = M.f32_to_bf16(rng.uniform(0.2, 2.0, H).astype(np.float32))
+    for eps in (1e-6, 1e-2):
+        assert np.array_equal(M.rms_norm(x, w, eps), _c_rms_norm(x, w, np.float32(eps)))
+
+
+def test_rms_norm_closed_forms():
+    """A row of one repeated value c has mean square c^2 exactly (for these
+    c the sum is exact), so with eps = 0 the output is bf16(sign(c) w); with
+    unit weights and eps = 0, sum n^2 = H to a few bf16 steps; the float64
+    formula agrees within the two bf16 roundings."""
+    H = 1024
+    w = M.f32_to_bf16(np.linspace(0.5, 1.5, H).astype(np.float32))
+    for c in (0.75, -3.0, 2.0 ** -10):
+        x = M.f32_to_bf16(np.full((1, H), c, np.float32))
+        y = M.rms_norm(x, w, 0.0)
+        assert np.array_equal(y[0], M.f32_to_bf16(np.sign(c) * M.bf16_to_f32(w)))
+    rng = np.random.default_rng(1)
+    x = M.f32_to_bf16(rng.standard_normal((4, H)).astype(np.float32))
+    ones = M.f32_to_bf16(np.ones(H, np.float32))
+    n = M.bf16_to_f32(M.rms_norm(x, ones, 0.0)).astype(np.float64)
+    assert np.allclose((n ** 2).sum(1), H, rtol=2.0 ** -7)
+    xf = M.bf16_to_f32(x).astype(np.float64)
+    exact = xf / np.sqrt((xf ** 2).mean(1, keepdims=True) + 1e-6) * M.bf16_to_f32(w)
+    got = M.bf16_to_f32(M.rms_norm(x, w, 1e-6))
+    assert np.all(np.abs(got - exact) <= np.abs(exact) * 2.0 ** -7 + 1e-30)
+
+
+def test_normed_block_numpy_and_c_agree():
+    L = M.make_layer(80, hidden=512, inter=128, experts=32, top_k=4, bits=8)
+    L.post_norm_w = M.f32_to_bf16(np.random.default_rng(2).uniform(0.5, 1.5, 512)
+                                  .astype(np.float32))
+    x = M.f32_to_bf16((np.random.default_rng(3).standard_normal((6, 512)) * 4)
+                      .astype(np.float32))
+    a, ia, _ = M.block_forward(L, x, residual_bits=x)
+    b, ib, _ = M.c_block_forward(L, x, residual_bits=x)
+    assert np.array_equal(ia, ib)
+    assert (a == b).mean() > 0.98
+    # the block saw the normalised input: routing equals that of rms_norm(x)
+    _, i2, _ = M.block_forward(M.Layer(**{**L.__dict__, "post_norm_w": None}),
+                               M.rms_norm(x, L.post_norm_w, L.norm_eps))
+    assert np.array_equal(ia, i2)
