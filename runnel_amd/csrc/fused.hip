@@ -318,6 +318,20 @@ __device__ __forceinline__ float gate_partial(const GateRow<1>& r, const float* 
   return acc;
 }
 
+// Descriptor of layer l.  The table is read through the constant address
+// space so the loads are scalar (uniform, read-only for the whole launch):
+// waiting for them does not wait for the vector loads in flight, which a
+// generic (flat) load of the descriptor would.
+typedef const FusedLayer __attribute__((address_space(4)))* ConstLayerPtr;
+__device__ __forceinline__ FusedLayer layer_desc(const FusedArgs& p, int l) {
+  if (!p.table) return p.layer0;
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass only parses device code
+  return reinterpret_cast<ConstLayerPtr>(reinterpret_cast<uintptr_t>(p.table))[l];
+#else
+  return p.table[l];
+#endif
+}
+
 // Whether the layer's shared expert has a sigmoid gate (its row pointer is
 // set).  Taken from the layer descriptor rather than a launch-wide flag: the
 // per-layer test keeps the compiler's schedule of the layer loop (a uniform
@@ -431,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   GateRow<RQ> rw, sw;  // router row; shared gate row (wave kPollWave)
   uint2 nw = make_uint2(0, 0);  // RMSNorm weights of values 4 t .. 4 t + 3
   {
-    const FusedLayer L0 = p.table ? p.table[0] : p.layer0;
+    const FusedLayer L0 = layer_desc(p, 0);
     // the norm weights first: the oldest load is the first one waited for
     if constexpr (NORM) nw = *reinterpret_cast<const uint2*>(L0.norm_w + 4 * threadIdx.x);
     issue_router_and_shared_down<BITS, RQ>(L0, row, E, p.has_shared, h, lane0,
@@ -449,7 +463,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     // would keep them live across all layers and spill them).
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    const FusedLayer L = p.table ? p.table[layer] : p.layer0;
+    const FusedLayer L = layer_desc(p, layer);
     const bool first = layer == 0;
     const bool last = layer == p.n_layers - 1;
     const uint32_t tag_logit = base + phase + 1;
@@ -684,6 +698,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
                                                 wave - (kWaves - kActPollWaves), timed_out);
     __syncthreads();
 
+    // The next layer's descriptor (scalar loads) before this layer's output
+    // stores: read after them, it waited for the stores to complete.
+    const FusedLayer Ln = layer_desc(p, last ? layer : layer + 1);
+
     // ---- D: down row h of every unit from registers.
     if (h < H) {
       float ys[NU];
@@ -746,7 +764,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     // x is polled by waves 4-7 and act by 2-7; the logits by wave 0, whose
     // extra loads (shared gate row, shared pairs) are back by then.
     if (!last) {
-      const FusedLayer Ln = p.table ? p.table[layer + 1] : p.layer0;
       if constexpr (NORM) nw = *reinterpret_cast<const uint2*>(Ln.norm_w + 4 * threadIdx.x);
       issue_router_and_shared_down<BITS, RQ>(Ln, row, E, p.has_shared, h, lane,
                                              wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
