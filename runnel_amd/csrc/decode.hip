@@ -284,142 +284,96 @@ __global__ __launch_bounds__(256) void router_split_kernel(const DecodeArgs p, u
 typedef __bf16 bf16x8_r __attribute__((ext_vector_type(8)));
 typedef float f32x4_r __attribute__((ext_vector_type(4)));
 
-// One wave: 16 tokens x 64 experts, K in chunks of 64 (four chunks of
-// loads in flight per lane); lane (col, g) holds A row / B column `col` and
-// k = 16 g + [0, 16) of each chunk.  ACC: continue the sums already in
-// `logits` (the second plane of a split gate).
-template <bool ACC>
-__global__ __launch_bounds__(64) void router_logits16_kernel(const DecodeArgs p) {
-  const int lane = threadIdx.x;
+// Matrix-core router logits: a workgroup takes 16 TB tokens x 64 experts and
+// splits K over its KS waves (wave w: chunks [w n / KS, (w + 1) n / KS) of
+// 64 values, D chunks of loads in flight); lane (col, g) holds A row / B
+// column `col` and k = 16 g + [0, 16) of each chunk.  The waves' partial
+// tiles meet in LDS and are added in wave order, after the sums already in
+// `logits` for ACC (the second plane of a split gate).  Splitting K keeps
+// every wave's chain of dependent loads short: the tile of one wave walking
+// all of K waited for a memory round trip every few chunks.
+template <int TB, int KS, int D, bool ACC>
+__global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs p) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int g = lane >> 4;
-  const int t0 = blockIdx.x * 16;
+  const int t0 = blockIdx.x * 16 * TB;
   const int e0 = blockIdx.y * 64;
-  const int tr = min(t0 + col, p.T - 1);
-  const uint16_t* xa = p.x + (size_t)tr * p.H + g * 16;
-  const uint16_t* wb[4];
+  const uint16_t* xa[TB];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) wb[cb] = p.router_w + (size_t)(e0 + cb * 16 + col) * p.H + g * 16;
-  f32x4_r acc[4];
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    acc[cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
-    if constexpr (ACC) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t0 + 4 * g + i;
-        if (t < p.T) acc[cb][i] = p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col];
-      }
-    }
-  }
-  const int nch = p.H / 64;
-  for (int c0 = 0; c0 < nch; c0 += 4) {
-    u32x4 a[4][2], b[4][4][2];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        a[u][j] = *reinterpret_cast<const u32x4*>(xa + (c0 + u) * 64 + 8 * j);
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-          b[u][cb][j] = *reinterpret_cast<const u32x4*>(wb[cb] + (c0 + u) * 64 + 8 * j);
-      }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-          acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_r, a[u][j]), __builtin_bit_cast(bf16x8_r, b[u][cb][j]),
-              acc[cb], 0, 0, 0);
-  }
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + 4 * g + i;
-      if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col] = acc[cb][i];
-    }
-}
-
-// Long prefills: one wave takes 64 tokens x 64 experts (4 x 4 MFMA tiles),
-// so each router row is read once per 64 tokens; K in chunks of 64 with the
-// next chunk's loads in flight, same lane layout.
-template <bool ACC>
-__global__ __launch_bounds__(64) void router_logits64_kernel(const DecodeArgs p) {
-  constexpr int kRouterTB = 4;  // 16-token blocks per wave
-  const int lane = threadIdx.x;
-  const int col = lane & 15;
-  const int g = lane >> 4;
-  const int t0 = blockIdx.x * 16 * kRouterTB;
-  const int e0 = blockIdx.y * 64;
-  const uint16_t* xa[kRouterTB];
-#pragma unroll
-  for (int tb = 0; tb < kRouterTB; ++tb)
+  for (int tb = 0; tb < TB; ++tb)
     xa[tb] = p.x + (size_t)min(t0 + tb * 16 + col, p.T - 1) * p.H + g * 16;
   const uint16_t* wb[4];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) wb[cb] = p.router_w + (size_t)(e0 + cb * 16 + col) * p.H + g * 16;
-  f32x4_r acc[kRouterTB][4];
+  f32x4_r acc[TB][4];
 #pragma unroll
-  for (int tb = 0; tb < kRouterTB; ++tb)
+  for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
-      if constexpr (ACC) {
+    for (int cb = 0; cb < 4; ++cb) acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+  const int per = p.H / 64 / KS;  // the host checks H % (64 KS) == 0
+  const int c_begin = wave * per;
+  const int c_end = c_begin + per;
+  for (int c0 = c_begin; c0 < c_end; c0 += D) {
+    u32x4 a[D][TB][2], b[D][4][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = t0 + tb * 16 + 4 * g + i;
-          if (t < p.T) acc[tb][cb][i] = p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col];
+    for (int u = 0; u < D; ++u) {
+      if (c0 + u < c_end) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int tb = 0; tb < TB; ++tb)
+            a[u][tb][j] = *reinterpret_cast<const u32x4*>(xa[tb] + (c0 + u) * 64 + 8 * j);
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+            b[u][cb][j] = *reinterpret_cast<const u32x4*>(wb[cb] + (c0 + u) * 64 + 8 * j);
         }
       }
     }
-  auto load = [&](int c, u32x4 (&a)[kRouterTB][2], u32x4 (&b)[4][2]) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int u = 0; u < D; ++u) {
+      if (c0 + u < c_end) {
 #pragma unroll
-      for (int tb = 0; tb < kRouterTB; ++tb)
-        a[tb][j] = *reinterpret_cast<const u32x4*>(xa[tb] + c * 64 + 8 * j);
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-        b[cb][j] = *reinterpret_cast<const u32x4*>(wb[cb] + c * 64 + 8 * j);
-    }
-  };
-  const int nch = p.H / 64;
-  u32x4 a[kRouterTB][2], b[4][2];
-  load(0, a, b);
-  for (int c = 0; c < nch; ++c) {
-    u32x4 na[kRouterTB][2], nb[4][2];
-    load(min(c + 1, nch - 1), na, nb);  // the last chunk loads itself again
+          for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int tb = 0; tb < kRouterTB; ++tb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-          acc[tb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_r, a[tb][j]), __builtin_bit_cast(bf16x8_r, b[cb][j]),
-              acc[tb][cb], 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int tb = 0; tb < kRouterTB; ++tb) a[tb][j] = na[tb][j];
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb) b[cb][j] = nb[cb][j];
+            for (int cb = 0; cb < 4; ++cb)
+              acc[tb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_r, a[u][tb][j]),
+                  __builtin_bit_cast(bf16x8_r, b[u][cb][j]), acc[tb][cb], 0, 0, 0);
+      }
     }
   }
+  __shared__ f32x4_r s_part[KS][TB * 4][64];
 #pragma unroll
-  for (int tb = 0; tb < kRouterTB; ++tb)
+  for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < 4; ++cb) s_part[wave][tb * 4 + cb][lane] = acc[tb][cb];
+  __syncthreads();
+  // tile blocks (tb, cb) are summed by waves in turn
+  for (int blk = wave; blk < TB * 4; blk += KS) {
+    const int tb = blk >> 2;
+    const int cb = blk & 3;
+    const int e = e0 + cb * 16 + col;
+    f32x4_r r = f32x4_r{0.f, 0.f, 0.f, 0.f};
+    if constexpr (ACC) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = t0 + tb * 16 + 4 * g + i;
-        if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e0 + cb * 16 + col] = acc[tb][cb][i];
+        if (t < p.T) r[i] = p.logits[(size_t)t * (p.E + 1) + e];
       }
+    }
+#pragma unroll
+    for (int w = 0; w < KS; ++w) r += s_part[w][blk][lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + tb * 16 + 4 * g + i;
+      if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e] = r[i];
+    }
+  }
 }
-
 
 // The router contract's dot of one token row (held as xv, chunk lane + 64 c
 // per lane) with one weight row.
@@ -915,6 +869,8 @@ bool router_mfma_eligible(int E, int H) {
 
 hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split,
                               hipStream_t s) {
+  // 64-token tiles from 4096 tokens on (each router row read once per 64
+  // tokens), K over 4 waves; shorter prefills 16-token tiles, K over 8 waves
   const dim3 g16((a.T + 15) / 16, a.E / 64), g64((a.T + 63) / 64, a.E / 64);
   const bool wide = a.T >= 4096;
   if (a.rq8) {
@@ -925,20 +881,20 @@ hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split
     hi.router_w = split;
     lo.router_w = split + (size_t)a.E * a.H;
     if (wide) {
-      hipLaunchKernelGGL(router_logits64_kernel<false>, g64, dim3(64), 0, s, hi);
-      hipLaunchKernelGGL(router_logits64_kernel<true>, g64, dim3(64), 0, s, lo);
+      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false>), g64, dim3(256), 0, s, hi);
+      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, true>), g64, dim3(256), 0, s, lo);
     } else {
-      hipLaunchKernelGGL(router_logits16_kernel<false>, g16, dim3(64), 0, s, hi);
-      hipLaunchKernelGGL(router_logits16_kernel<true>, g16, dim3(64), 0, s, lo);
+      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false>), g16, dim3(512), 0, s, hi);
+      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, true>), g16, dim3(512), 0, s, lo);
     }
     hipLaunchKernelGGL(router_select_kernel<1>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   } else {
     hipLaunchKernelGGL(router_rownorm_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, wnorm);
     if (wide)
-      hipLaunchKernelGGL(router_logits64_kernel<false>, g64, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false>), g64, dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL(router_logits16_kernel<false>, g16, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false>), g16, dim3(512), 0, s, a);
     hipLaunchKernelGGL(router_select_kernel<0>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   }

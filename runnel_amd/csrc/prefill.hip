@@ -26,10 +26,10 @@
 //                           the gated shared row, residual, bf16.
 //
 // Tiles are 32 rows (short prefill: memory bound, few rows per expert) or
-// 128 rows (long prefill: matrix-core bound).  A workgroup is 8 waves (two
-// per SIMD: a single wave per SIMD issues vector instructions too slowly to
-// keep the dequantisation beside the MFMAs); each wave owns 32 weight
-// columns of the tile.
+// 128 rows (long prefill: matrix-core bound).  A workgroup is 8 waves, 4 for
+// the short gate/up tiles (at least two waves per SIMD: a single wave per
+// SIMD issues vector instructions too slowly to keep the dequantisation
+// beside the MFMAs); each wave owns 32 weight columns of the tile.
 //
 // MFMA operand layout (16x16x32 bf16, checked on the device): lane l holds
 // A row l % 16 and B column l % 16, k = 8 (l / 16) + [0, 8); D column l % 16,
@@ -61,7 +61,10 @@ constexpr int kPad = 8;                         // bf16 of padding per LDS row
 // (32-row tiles over K = H, a multiple of 256), else 128.
 template <int BITS, int BM, int MODE>
 struct Chunk {
-  static constexpr int THREADS = 512;                  // 8 waves
+  // 8 waves, except the short prefill's gate/up tiles: 4 waves (64 pairs),
+  // four workgroups per CU, so the last partial round of tiles is half as
+  // long (the shared expert's tiles make the count just over a round)
+  static constexpr int THREADS = BM == 32 && MODE == 0 ? 256 : 512;
   static constexpr int QPW = 2;                        // 16-column blocks per wave
   static constexpr int MIN_WAVES = BM == 32 ? 4 : 2;   // waves per SIMD (registers)
   static constexpr int KC = BITS == 8 ? 128 : ((BM == 32 && MODE == 0) ? 256 : 128);
