@@ -12,7 +12,9 @@ the previous step's output, so the routing changes from token to token.
 
 Prints one JSON line.  `value` is microseconds per MoE layer per token
 (lower is better); `hbm_gbps` is the algorithmic bytes of a layer divided
-by that time; `roofline` relates the same quantity to MI355X's 8 TB/s.
+by that time; `roofline` relates the same quantity to MI355X's 8 TB/s and
+(`frac_of_measured_read`) to the read bandwidth a plain 16-byte-load stream
+reaches on the same box, measured in the same run.
 
 `roofline` is priced per launch of the dominant kernel (fused_decode_kernel,
 one launch per token carrying all 40 layers): algorithmic bytes of 40 layers
@@ -88,6 +90,30 @@ def calibrate_copy(torch, gib: int = 1, reps: int = 5):
     print(json.dumps({"calibration": "bitwise_not int32", "bytes_read": n * 4,
                       "bytes_written": n * 4, "launches": reps}), flush=True)
     return 0
+
+
+def measured_read_gbps(torch, gib: int = 4, reps: int = 10):
+    """The box's achievable HBM read bandwidth: rmoe_stream_read (16-byte
+    loads, every byte once) over a buffer far larger than the 256 MB MALL,
+    best launch shape of a small sweep, HIP events on the current stream."""
+    from runnel_amd import native
+    buf = torch.empty(gib << 30, dtype=torch.uint8, device="cuda")
+    best = 0.0
+    for blocks in (2048, 4096, 8192):
+        part = torch.empty(blocks, dtype=torch.int32, device="cuda")
+        native.stream_read(buf, blocks, part)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            native.stream_read(buf, blocks, part)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / reps
+        best = max(best, buf.numel() / us / 1e3)
+    del buf
+    return best
 
 
 def median(v):
@@ -292,6 +318,7 @@ def main():
         print(json.dumps({"workload": args.workload, **r}), flush=True)
         return 0
     res = run_decode_chain(args, torch)
+    read_gbps = measured_read_gbps(torch)
     launch_bytes = res["layer_bytes"] * args.layers
     achieved = launch_bytes / (res["us_token"] * 1e-6) / 1e9
     traffic = (recorded_traffic(args.layers, args.bits)
@@ -332,6 +359,10 @@ def main():
             "traffic": traffic,
             "bytes_per_launch": launch_bytes,
             "us_per_launch": round(res["us_token"], 3),
+            # the same achieved rate against what a pure read stream reaches
+            # on this box (rmoe_stream_read over 4 GiB)
+            "measured_read_gbps": round(read_gbps, 1),
+            "frac_of_measured_read": round(achieved / read_gbps, 4),
         },
     }
     if not args.no_prefill:
