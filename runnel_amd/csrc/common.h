@@ -85,57 +85,89 @@ __device__ __forceinline__ float segment_sum_fast(float v, int width) {
   return v;
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint32_t o = __shfl_xor(v, d, kWave);
-    v = o > v ? o : v;
+// Wave maximum of unsigned keys: rows of 16 by DPP, then across row pairs
+// and halves with the gfx950 permlane swaps (VALU, no LDS round trip);
+// every lane ends with the maximum.
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v, int ctrl) {
+  switch (ctrl) {
+    case 0xB1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    case 0x4E: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    case 0x141: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);
   }
-  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u(v, 0xB1));
+  v = max(v, dpp_u(v, 0x4E));
+  v = max(v, dpp_u(v, 0x141));
+  v = max(v, dpp_u(v, 0x140));
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(b[0], b[1]);
+}
+
+// Each lane's P keys in descending order (odd-even transposition network).
+template <int P>
+__device__ __forceinline__ void sort_desc(uint32_t (&k)[P]) {
+#pragma unroll
+  for (int r = 0; r < P; ++r)
+#pragma unroll
+    for (int i = r & 1; i + 1 < P; i += 2) {
+      const uint32_t hi = k[i] > k[i + 1] ? k[i] : k[i + 1];
+      const uint32_t lo = k[i] > k[i + 1] ? k[i + 1] : k[i];
+      k[i] = hi;
+      k[i + 1] = lo;
+    }
+}
+
+// The lanes whose largest remaining key equals `best` drop it.
+template <int P>
+__device__ __forceinline__ void pop_head(uint32_t (&k)[P], uint32_t best) {
+  if (k[0] == best) {
+#pragma unroll
+    for (int i = 0; i + 1 < P; ++i) k[i] = k[i + 1];
+    k[P - 1] = 0;
+  }
 }
 
 // ------------------------------------------------------------ top-k keys
 // Keys are unique and nonzero: (bf16 order key << 16) | (0xFFFF - index), so
-// "larger key" = larger logit, then lower index.  Selects the k largest of
-// the P keys per lane (absent keys are 0) without serial max rounds: a
-// 32-step ballot search finds the k-th largest key, the selected keys are
-// compacted into `lds[0..k)` and ranked.  Must be called by a whole wave;
-// returns, in lane j < k, the key of rank j (descending).
+// "larger key" = larger logit, then lower index.  The k largest of the P
+// keys per lane (absent keys are 0): each lane sorts its keys, then k
+// rounds of a wave maximum over the lanes' largest remaining keys.  Must be
+// called by a whole wave; returns, in lane j < k, the key of rank j
+// (descending).  (A 32-step ballot search for the k-th key took about
+// three times as long: every step waits for a compare, a ballot and a
+// scalar count in turn.)
 template <int P>
-__device__ __forceinline__ uint32_t wave_topk(const uint32_t (&keys)[P], int k,
-                                              uint32_t* lds) {
+__device__ __forceinline__ uint32_t wave_topk(uint32_t (&keys)[P], int k) {
   const int lane = threadIdx.x & 63;
-  uint32_t thr = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < P; ++i) cnt += __popcll(__ballot(keys[i] >= cand));
-    if (cnt >= k) thr = cand;
-  }
-  int before = 0;
-  const unsigned long long lt = (1ull << lane) - 1ull;
-#pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const bool sel = keys[i] >= thr && keys[i] != 0u;
-    const unsigned long long m = __ballot(sel);
-    if (sel) lds[before + __popcll(m & lt)] = keys[i];
-    before += __popcll(m);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
+  sort_desc<P>(keys);
   uint32_t mine = 0;
-  int rank = 0;
-  if (lane < k) {
-    mine = lds[lane];
-    for (int j = 0; j < k; ++j) rank += lds[j] > mine ? 1 : 0;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t best = wave_max_u32(keys[0]);
+    if (lane == j) mine = best;
+    pop_head<P>(keys, best);
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  if (lane < k) lds[64 + rank] = mine;
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  return lane < k ? lds[64 + lane] : 0u;
+  return mine;
+}
+
+// The k-th largest of the P keys per lane counted with multiplicity (keys
+// may repeat; absent keys are 0): rounds of a wave maximum over the lanes'
+// largest remaining keys, every lane holding that maximum dropping it,
+// until k keys have been dropped (at most k rounds).
+template <int P>
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t (&keys)[P], int k) {
+  sort_desc<P>(keys);
+  int taken = 0;
+  uint32_t best = 0;
+  while (taken < k) {
+    best = wave_max_u32(keys[0]);
+    taken += __popcll(__ballot(keys[0] == best));
+    pop_head<P>(keys, best);
+  }
+  return best;
 }
 
 // ------------------------------------------------------- packed dot chunks

@@ -23,7 +23,7 @@ namespace rmoe {
 // shared-expert gate's fp32 logit.  One wave.
 template <int P>
 __device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const float (&lv)[P],
-                                             float sg_logit, uint32_t* s_topk) {
+                                             float sg_logit) {
   const int lane = threadIdx.x & 63;
   uint32_t keys[P];
 #pragma unroll
@@ -32,7 +32,7 @@ __device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const f
     keys[i] = e < p.E ? (bf16_order_key(f32_to_bf16(lv[i])) << 16) | (0xFFFFu - (uint32_t)e)
                       : 0u;
   }
-  const uint32_t my_key = wave_topk<P>(keys, p.K, s_topk);
+  const uint32_t my_key = wave_topk<P>(keys, p.K);
   const uint32_t top_key = __builtin_amdgcn_readfirstlane(my_key);
   const float m = bf16_to_f32(bf16_from_order_key(top_key >> 16));
   float z = 0.0f;
@@ -45,7 +45,8 @@ __device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const f
   float pb = 0.0f;
   if (lane < p.K) pb = round_bf16(__expf(my_logit - m) / z);
   float total = 0.0f;
-  for (int j = 0; j < p.K; ++j) total += __shfl(pb, j, 64);
+  for (int j = 0; j < p.K; ++j)
+    total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
   const float score = p.norm ? round_bf16(pb / total) : pb;
   if (lane < p.K) {
     p.idx[t * p.K + lane] = my_sel;
@@ -166,7 +167,6 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
 
   // Last workgroup of this token ranks the logits.
   __shared__ uint32_t s_last;
-  __shared__ uint32_t s_topk[128];
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
     lv[i] = e < p.E ? round_bf16(load_coherent(lg + e)) : 0.0f;
   }
   const float sg_logit = has_sg ? load_coherent(lg + p.E) : 0.0f;
-  finish_route<P>(p, t, lv, sg_logit, s_topk);
+  finish_route<P>(p, t, lv, sg_logit);
   if (lane == 0)
     __hip_atomic_store(&p.ctr[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -446,7 +446,6 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
                                                             const float* wnorm) {
   constexpr int P = 4;
   constexpr int XC = 8;
-  __shared__ uint32_t s_topk[4][128];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wave;
@@ -492,14 +491,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
   wn = __uint_as_float(wave_max_u32(__float_as_uint(wn)));      // non-negative
   amax = __uint_as_float(wave_max_u32(__float_as_uint(amax)));
   // k-th largest L (with multiplicity)
-  uint32_t thr = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < P; ++i) cnt += __popcll(__ballot(key[i] >= cand));
-    if (cnt >= p.K) thr = cand;
-  }
+  const uint32_t thr = wave_kth_largest<P>(key, p.K);
   const float tk = f32_from_order_key(thr);
   const float gam =
       RQ ? (float)(2 * p.H - 1) * 0x1p-23f * (1.0f + 0x1p-7f) + 0x1p-17f +
@@ -529,7 +521,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
   float sg_logit = 0.0f;
   if (p.has_sg)
     sg_logit = RQ ? q8_contract_dot(xv, p.sgq, 0, p.H) : contract_dot<XC>(xv, nxc, p.sgate_w);
-  finish_route<P>(p, t, out, sg_logit, s_topk[wave]);
+  finish_route<P>(p, t, out, sg_logit);
 }
 
 // ----------------------------------------------------------------- RMSNorm

@@ -67,28 +67,6 @@ __device__ __forceinline__ bool tag_ok(uint32_t word, uint32_t tag) {
 constexpr int kXcdLoadAux = 3;   // sc0 | nt
 constexpr int kXcdStoreAux = 1;  // sc0
 
-// Wave maximum of unsigned keys with the DPP pattern of wave_sum; the
-// result is uniform.
-__device__ __forceinline__ uint32_t dpp_u(uint32_t v, int ctrl) {
-  switch (ctrl) {
-    case 0xB1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
-    case 0x4E: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
-    case 0x141: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false);
-    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);
-  }
-}
-__device__ __forceinline__ uint32_t wave_max_fast(uint32_t v) {
-  // rows of 16 by DPP, then across row pairs and halves with the gfx950
-  // permlane swaps (VALU, no LDS round trip): every lane ends with the max
-  v = max(v, dpp_u(v, 0xB1));
-  v = max(v, dpp_u(v, 0x4E));
-  v = max(v, dpp_u(v, 0x141));
-  v = max(v, dpp_u(v, 0x140));
-  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = max(a[0], a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return max(b[0], b[1]);
-}
 // One wave collects n_words tagged words written by other workgroups: 16-byte
 // loads at agent coherence (sc1, the bits agent-scope atomic loads use; each
 // 4-byte word is as one store left it), repeated only for the pieces whose
@@ -566,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       for (int j = 0; j < NU - 1; ++j) {
         sel[j] = 0;
         if (j < K) {
-          const uint32_t best = wave_max_fast(k[0]);
+          const uint32_t best = wave_max_u32(k[0]);
           sel[j] = best;
           if (k[0] == best) {
             k[0] = k[1];
