@@ -54,15 +54,18 @@ def qweight_struct(weight, scales, biases, bits: int, group_size: int = 64) -> _
 
 
 class Workspace:
-    """Grow-only, zero-initialised device scratch per (device, purpose).
-    The library keeps its counters at zero between calls, so the buffer is
-    zeroed only when it is (re)allocated."""
+    """Grow-only, zero-initialised device scratch per (device, stream,
+    purpose).  The library keeps its counters at zero between calls, so the
+    buffer is zeroed only when it is (re)allocated.  Calls on one stream run
+    in order and may share a buffer; calls on different streams may overlap,
+    so each stream gets its own (the library's calls are safe concurrently
+    on different streams only with different workspaces)."""
 
     def __init__(self):
         self._bufs: dict = {}
 
     def get(self, device, nbytes: int, key: str = "default") -> torch.Tensor:
-        k = (str(device), key)
+        k = (str(device), torch.cuda.current_stream(device).cuda_stream, key)
         buf = self._bufs.get(k)
         if buf is None or buf.numel() < nbytes:
             # 256-byte alignment comes from the caching allocator (512 B).

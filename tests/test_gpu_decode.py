@@ -206,3 +206,29 @@ def test_block_full_shape_decode(torch_cuda, bits):
     g = M.bf16_to_f32(got)
     assert np.abs(g - M.bf16_to_f32(mlx)).max() <= MAX_ABS
     assert cosine(g, M.bf16_to_f32(mlx)) >= MIN_COS
+
+
+def test_calls_on_two_streams_use_separate_workspaces(torch_cuda):
+    """Calls issued on two streams at once (the router/gate-up/down kernels
+    at 5 tokens, the expert-sorted path at 100) give the results of the
+    same calls made one after another: each stream has its own workspace."""
+    torch = torch_cuda
+    from runnel_amd import native
+    L = M.make_layer(7100, hidden=512, inter=128, experts=32, top_k=4, bits=8)
+    h = layer_to_dev(L)
+    xs = [dev_bf16(M.make_x(7101 + i, T, 512)) for i, T in enumerate((5, 100, 5, 100))]
+    ref = [native.moe_block(h, x) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    got = [None] * len(xs)
+    for rep in range(3):
+        for i, x in enumerate(xs):
+            with torch.cuda.stream(streams[i % 2]):
+                got[i] = native.moe_block(h, x)
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for g, r in zip(got, ref):
+        assert torch.equal(g, r)
