@@ -216,25 +216,6 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
 // exact bf16 logits for all candidates.  Experts outside the margin keep
 // bf16(L) (they only enter the softmax denominator).
 
-__global__ __launch_bounds__(256) void router_rownorm_kernel(const DecodeArgs p, float* wnorm) {
-  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (e >= p.E) return;
-  const uint16_t* w = p.router_w + (size_t)e * p.H;
-  float s = 0.0f;
-  for (int c = lane; c < p.H / 8; c += 64) {
-    const uint4 v = load16(w + c * 8);
-    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      s = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), s);
-      s = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), s);
-    }
-  }
-  s = wave_sum(s);
-  if (lane == 0) wnorm[e] = sqrtf(s) * (1.0f + 1.0f / 1024.0f);
-}
-
 // 8-bit gate rows as two bf16 planes hi = bf16(w), lo = bf16(w - hi) of
 // w = fl32(q s + b) (w - hi is exact), and the row bound
 // || |q s| + |b| ||_2.  One wave per row, 16 codes per lane and step.
@@ -291,9 +272,13 @@ typedef float f32x4_r __attribute__((ext_vector_type(4)));
 // tiles meet in LDS and are added in wave order, after the sums already in
 // `logits` for ACC (the second plane of a split gate).  Splitting K keeps
 // every wave's chain of dependent loads short: the tile of one wave walking
-// all of K waited for a memory round trip every few chunks.
-template <int TB, int KS, int D, bool ACC>
-__global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs p) {
+// all of K waited for a memory round trip every few chunks.  WNORM: the
+// workgroups of the first token tile also write the bound ||w_e||_2 (1 +
+// 2^-10) of their 64 router rows into wnorm from the rows they stream (the
+// padding covers any order of the fp32 sum of squares).
+template <int TB, int KS, int D, bool ACC, bool WNORM>
+__global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs p,
+                                                                float* wnorm) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -312,6 +297,8 @@ __global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs
   for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+  const bool norms = WNORM && blockIdx.x == 0;
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's squares of rows cb
   const int per = p.H / 64 / KS;  // the host checks H % (64 KS) == 0
   const int c_begin = wave * per;
   const int c_end = c_begin + per;
@@ -331,6 +318,23 @@ __global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs
         }
       }
     }
+    if (norms) {
+#pragma unroll
+      for (int u = 0; u < D; ++u)
+        if (c0 + u < c_end)
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const u32x4 w = b[u][cb][j];
+              const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                ss[cb] = fmaf(bf16_lo(ww[i]), bf16_lo(ww[i]), ss[cb]);
+                ss[cb] = fmaf(bf16_hi(ww[i]), bf16_hi(ww[i]), ss[cb]);
+              }
+            }
+    }
 #pragma unroll
     for (int u = 0; u < D; ++u) {
       if (c0 + u < c_end) {
@@ -347,11 +351,27 @@ __global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs
     }
   }
   __shared__ f32x4_r s_part[KS][TB * 4][64];
+  __shared__ float s_ss[WNORM ? KS : 1][4][64];
 #pragma unroll
   for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) s_part[wave][tb * 4 + cb][lane] = acc[tb][cb];
+  if (norms) {
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) s_ss[wave][cb][lane] = ss[cb];
+  }
   __syncthreads();
+  if (norms && wave == KS - 1) {
+    // lane l: row cb = l / 16, column col = l % 16, summed over the four
+    // k groups and the waves
+    const int cb = lane >> 4;
+    float n2 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < KS; ++w)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) n2 += s_ss[w][cb][gg * 16 + (lane & 15)];
+    wnorm[e0 + lane] = sqrtf(n2) * (1.0f + 1.0f / 1024.0f);
+  }
   // tile blocks (tb, cb) are summed by waves in turn
   for (int blk = wave; blk < TB * 4; blk += KS) {
     const int tb = blk >> 2;
@@ -873,20 +893,26 @@ hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split
     hi.router_w = split;
     lo.router_w = split + (size_t)a.E * a.H;
     if (wide) {
-      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false>), g64, dim3(256), 0, s, hi);
-      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, true>), g64, dim3(256), 0, s, lo);
+      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false, false>), g64, dim3(256), 0, s, hi,
+                         nullptr);
+      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, true, false>), g64, dim3(256), 0, s, lo,
+                         nullptr);
     } else {
-      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false>), g16, dim3(512), 0, s, hi);
-      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, true>), g16, dim3(512), 0, s, lo);
+      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false, false>), g16, dim3(512), 0, s, hi,
+                         nullptr);
+      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, true, false>), g16, dim3(512), 0, s, lo,
+                         nullptr);
     }
     hipLaunchKernelGGL(router_select_kernel<1>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   } else {
-    hipLaunchKernelGGL(router_rownorm_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, wnorm);
+    // the row norms come from the first token tile's workgroups
     if (wide)
-      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false>), g64, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false, true>), g64, dim3(256), 0, s, a,
+                         wnorm);
     else
-      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false>), g16, dim3(512), 0, s, a);
+      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false, true>), g16, dim3(512), 0, s, a,
+                         wnorm);
     hipLaunchKernelGGL(router_select_kernel<0>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   }
