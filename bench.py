@@ -174,6 +174,8 @@ def run_decode_chain(args, torch):
         native.moe_chain(chain, bufs[i & 1], out=bufs[(i + 1) & 1], workspace=ws)
 
     step = launch
+    if args.launch == "eager-plain":
+        native.set_cooperative_launch(False)
     if args.launch == "graph":
         # the decode loop as a serving loop runs it: one captured HIP graph
         # per direction of the ping-pong buffers, each holding the one
@@ -288,9 +290,10 @@ def main():
                          "(h + MoE(RMSNorm(h)), the decoder's sequence)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
-                    help="replay captured HIP graphs (default) or launch eagerly "
-                         "(cooperative launch) every step")
+    ap.add_argument("--launch", choices=["graph", "eager", "eager-plain"], default="graph",
+                    help="replay captured HIP graphs (default), launch eagerly every "
+                         "step (cooperative launch), or eagerly with plain launches "
+                         "(rmoe_set_cooperative_launch(0))")
     ap.add_argument("--workload", choices=["decode40", "prefill512", "prefill8192"],
                     default="decode40",
                     help="decode40: the bench line; the prefill workloads print "

@@ -225,6 +225,19 @@ int rmoe_moe_chain(const rmoe_layer* layer0, const void* device_table,
  * still completes; its outputs are then not valid). */
 size_t rmoe_workspace_status_offset(void);
 
+/* Launch mode of the single-launch decode kernel (rmoe_moe_block with one
+ * token of the decode shape, rmoe_moe_chain) outside stream capture.
+ * enabled = 1 (the default): a cooperative launch, which guarantees every
+ * workgroup is resident whatever else runs on the device, but does not
+ * overlap the previous call (about 17 us more per call on MI355X).
+ * enabled = 0: a plain launch, as stream capture records it; valid while no
+ * other work runs on the device during the call (a workgroup left waiting
+ * for one that is not resident times out and sets the status word above).
+ * Process-wide; returns the previous mode.  No counterpart in the
+ * reference (its probes submit one Metal command buffer per call): for
+ * eager decode loops that own the device. */
+int rmoe_set_cooperative_launch(int32_t enabled);
+
 /* Affine quantization of fp32 rows [rows, cols] (group_size 64, bits 4|8):
  * per group, the larger-magnitude edge value is kept exact, scale and bias
  * are rounded to bf16 and the codes are round-half-even((w - b) / s)

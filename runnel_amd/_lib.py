@@ -31,6 +31,7 @@ EXPORTED = (
     "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes", "rmoe_chain_table_pack",
     "rmoe_moe_chain", "rmoe_workspace_status_offset", "rmoe_router_q",
     "rmoe_switch_combine", "rmoe_switch_combine_workspace_bytes", "rmoe_rms_norm",
+    "rmoe_set_cooperative_launch",
 )
 
 
@@ -120,6 +121,7 @@ def load() -> ctypes.CDLL:
         lib.rmoe_moe_chain.argtypes = [LP, P, I32, P, P, P, SZ, P]
         lib.rmoe_workspace_status_offset.restype = SZ
         lib.rmoe_workspace_status_offset.argtypes = []
+        lib.rmoe_set_cooperative_launch.argtypes = [I32]
         for name in EXPORTED:
             if name not in ("rmoe_last_error", "rmoe_status_string",
                             "rmoe_workspace_bytes", "rmoe_switch_workspace_bytes",

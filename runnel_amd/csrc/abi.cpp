@@ -4,6 +4,7 @@
 // memory.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstddef>
 #include <cstdio>
@@ -15,6 +16,7 @@
 namespace {
 
 thread_local std::string g_error;
+std::atomic<int> g_cooperative{1};  // rmoe_set_cooperative_launch
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -835,6 +837,12 @@ size_t rmoe_workspace_status_offset(void) {
   return layout(0, 1, 1, 0).fused + offsetof(rmoe::FusedScratch, err);
 }
 
+int rmoe_set_cooperative_launch(int32_t enabled) {
+  const int prev = g_cooperative.exchange(enabled ? 1 : 0);
+  ok();
+  return prev;
+}
+
 int rmoe_stream_read(const void* buffer, size_t bytes, uint32_t* partials,
                      int32_t blocks, void* stream) {
   if (!buffer || !partials) return fail(RMOE_ENULL, "buffer and partials are required");
@@ -849,3 +857,7 @@ int rmoe_stream_read(const void* buffer, size_t bytes, uint32_t* partials,
 }
 
 }  // extern "C"
+
+namespace rmoe {
+bool cooperative_launch_enabled() { return g_cooperative.load(std::memory_order_relaxed) != 0; }
+}  // namespace rmoe

@@ -799,11 +799,13 @@ hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream
   void* kargs[] = {&args};
   const void* fn = fused_fn(bits, a.rq8, a.rms_norm);
   // A cooperative launch guarantees every workgroup is resident.  Under
-  // stream capture a plain launch of the same one-workgroup-per-CU grid is
-  // recorded instead (every workgroup fits at once on an otherwise idle
-  // device; the bounded waits turn anything else into a status error).
+  // stream capture, or when the caller has turned cooperative launches off,
+  // a plain launch of the same one-workgroup-per-CU grid is made instead
+  // (every workgroup fits at once on an otherwise idle device; the bounded
+  // waits turn anything else into a status error).
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+  if (!cooperative_launch_enabled() ||
+      (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone))
     return hipLaunchKernel(fn, dim3(grid), dim3(kThreads), kargs, 0, s);
   return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kThreads), kargs, 0, s);
 }

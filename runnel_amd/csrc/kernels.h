@@ -104,6 +104,8 @@ struct FusedArgs {
 
 hipError_t fused_grid(int bits, int rq8, int rms_norm, int* grid);
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s);
+// rmoe_set_cooperative_launch's process-wide mode (abi.cpp).
+bool cooperative_launch_enabled();
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s);
 // RMSNorm of T rows of H bf16 values (H a multiple of 8; x, w, out 16-byte aligned).

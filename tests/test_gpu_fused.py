@@ -212,3 +212,26 @@ def test_thousand_step_4bit_decode(torch_cuda):
     g = M.bf16_to_f32(got)
     assert np.abs(g - M.bf16_to_f32(mlx)).max() <= MAX_ABS
     assert cosine(g, M.bf16_to_f32(mlx)) >= MIN_COS
+
+
+def test_plain_eager_launch_equals_cooperative(torch_cuda):
+    """Eager one-token calls with cooperative launches turned off (plain
+    launches that overlap the previous call) give the cooperative launches'
+    outputs bit for bit, and the status word stays clear."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lw = synthetic.make_layer(7300, bits=8)
+    h = lw.handle()
+    xs = synthetic.make_x(7301, 8, 2048)
+    ws = torch.zeros(h.workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    coop = [native.moe_block(h, xs[t:t + 1], workspace=ws) for t in range(8)]
+    prev = native.set_cooperative_launch(False)
+    try:
+        assert prev is True
+        plain = [native.moe_block(h, xs[t:t + 1], workspace=ws) for t in range(8)]
+        torch.cuda.synchronize()
+    finally:
+        native.set_cooperative_launch(True)
+    assert native.workspace_status(ws) == 0
+    for a, b in zip(coop, plain):
+        assert torch.equal(a, b)
