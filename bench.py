@@ -116,6 +116,12 @@ def measured_read_gbps(torch, gib: int = 4, reps: int = 10):
     return best
 
 
+def mad(v):
+    """Median absolute deviation from the median."""
+    m = median(v)
+    return median([abs(x - m) for x in v])
+
+
 def median(v):
     s = sorted(v)
     n = len(s)
@@ -263,6 +269,7 @@ def run_prefill(torch, tokens, bits, skewed, steps, warmup, seed=7):
     flops = prefill_flops(tokens, H, I, E, K)
     return {
         "tokens": tokens, "bits": bits, "skewed": skewed, "us": round(us, 1),
+        "us_mad": round(mad(times), 1),
         "tokens_per_s": round(tokens / (us * 1e-6), 1),
         "tflops": round(flops / (us * 1e-6) / 1e12, 1),
         "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -351,6 +358,7 @@ def main():
         "tokens_per_s": round(1e6 / res["us_token"], 2),
         "hbm_gbps": round(achieved, 1),
         "step_us_median": round(median(res["step_us"]), 2),
+        "step_us_mad": round(mad(res["step_us"]), 2),
         "roofline": {
             "bound": "hbm",
             "kernel": "fused_decode_kernel (whole chain in one launch; per layer: router, "
