@@ -126,7 +126,11 @@ def test_block_prefill_512_tokens_8bit(torch_cuda):
 
 
 @pytest.mark.parametrize("shape", [dict(hidden=1024, experts=128, top_k=8),
-                                   dict(hidden=512, experts=64, top_k=6)])
+                                   dict(hidden=512, experts=64, top_k=6),
+                                   # the widest eligible rows: two passes of
+                                   # four chunks per wave over K, x held in
+                                   # eight pieces per lane by the re-check
+                                   dict(hidden=4096, experts=64, top_k=4)])
 def test_matrix_core_router_selection_is_exact(torch_cuda, shape):
     """Many tokens route through the MFMA logits + exact re-check path:
     indices equal the oracle's bit for bit, scores within a bf16 step."""
