@@ -232,3 +232,20 @@ def test_sparse_moe_block_module_with_quantized_gate(torch_cuda):
     inds, _ = native.router((blk.gate.weight, blk.gate.scales, blk.gate.biases), dev_bf16(x), 4)
     torch.cuda.synchronize()
     assert np.array_equal(inds.cpu().numpy(), M.route(x, L.router_w, 4)[0])
+
+
+def test_prefill_router_widest_rows(torch_cuda):
+    """Hidden 4096 with an 8-bit gate, 160 tokens: both split planes
+    through the matrix-core logits (two passes over K per wave, the second
+    continuing the first's sums) and the 8-piece re-check select exactly the
+    oracle's experts."""
+    torch = torch_cuda
+    from runnel_amd import native
+    L = M.make_layer(340, hidden=4096, inter=128, experts=64, top_k=4, router_bits=8)
+    x = M.make_x(341, 160, 4096)
+    h = layer_to_dev(L)
+    _, idx, scores = native.moe_block(h, dev_bf16(x), return_routing=True)
+    torch.cuda.synchronize()
+    ref_idx, ref_scores, _ = M.route(x, L.router_w, 4)
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    assert np.abs(scores.cpu().numpy() - ref_scores).max() <= 2.0 ** -8
