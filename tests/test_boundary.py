@@ -403,3 +403,12 @@ def test_bench_byte_model_matches_the_survey_figures():
     # such row for the shared gate, instead of 257 bf16 rows
     q = bench.layer_bytes(2048, 512, 256, 8, 8, gate_bits=8)
     assert 31_141_888 - q == 257 * (4096 - (2048 + 128))
+
+
+def test_cooperative_launch_switch_returns_previous_mode():
+    """rmoe_set_cooperative_launch is process-wide and returns the previous
+    mode; cooperative launches are the default."""
+    lib = _lib.load()
+    assert lib.rmoe_set_cooperative_launch(0) == 1
+    assert lib.rmoe_set_cooperative_launch(7) == 0   # any nonzero turns it on
+    assert lib.rmoe_set_cooperative_launch(1) == 1
