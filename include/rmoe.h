@@ -58,6 +58,10 @@ extern "C" {
 #define RMOE_EWS (-4)    /* workspace missing or too small */
 #define RMOE_EHIP (-5)   /* the HIP runtime reported an error */
 #define RMOE_ENULL (-6)  /* a required pointer is NULL */
+/* Not returned by any call (the calls do not wait for the GPU): the code
+ * callers report when a workspace's status word (rmoe_workspace_status_offset)
+ * shows that a single-launch decode gave up a cross-workgroup wait. */
+#define RMOE_ETIMEOUT (-7)
 
 /* One MLX-affine quantized bank: w [experts, rows, cols*bits/32] u32,
  * scales / biases [experts, rows, cols/group_size] bf16. */
@@ -91,7 +95,11 @@ typedef struct rmoe_qweight {
  * front of the block (appended in ABI version 3): the block's input is
  * rmoe_rms_norm(x, post_norm_w, norm_eps), the residual stays what the
  * caller passes, so a decoder computes h' = h + MoE(RMSNorm(h)) with
- * residual = x = h (the layer sequence of docs/architecture.md:31-37). */
+ * residual = x = h (the layer sequence of docs/architecture.md:31-37).
+ *
+ * Shapes: hidden and inter multiples of 64; hidden at most 4096 at 8 bits
+ * (8192 at 4 bits); inter / (16 at 8 bits, 32 at 4 bits) a power of two
+ * <= 64; experts <= 1024; top_k <= min(64, experts). */
 typedef struct rmoe_layer {
   int32_t hidden;
   int32_t inter;
@@ -196,9 +204,12 @@ int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows,
  * score_j * y_j + bf16(sigmoid(x . shared_gate_w)) * y_shared); with
  * residual != NULL, out[t] = bf16(residual[t] + out[t]).  indices_out /
  * scores_out may be NULL.  x, residual, out bf16 [tokens, hidden]; out may
- * alias residual but not x.  Calls that route 64 or more (token, slot) rows
- * take the expert-sorted path, which needs out and residual 16-byte
- * aligned (2 bytes otherwise). */
+ * alias residual but not x.  One token of a layer with hidden 2048, inter
+ * 512, top_k <= 8 and experts <= 256 runs as one single-launch kernel (see
+ * rmoe_workspace_status_offset); other calls that route fewer than 64
+ * (token, slot) rows take the router, gate/up and down kernels; calls that
+ * route 64 or more take the expert-sorted path, which needs out and
+ * residual 16-byte aligned (2 bytes otherwise). */
 int rmoe_moe_block(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
                    const uint16_t* residual, uint16_t* out,
                    int32_t* indices_out, float* scores_out, void* workspace,
@@ -211,8 +222,9 @@ int rmoe_moe_block(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
  * The layer descriptors are packed once on the host with
  * rmoe_chain_table_pack into rmoe_chain_table_bytes(n) bytes, copied by the
  * caller to device memory, and passed as device_table; layer0 describes the
- * common shape.  Needs hidden 2048, inter 512, top_k + shared <= 9,
- * experts <= 512.  x, out bf16 [hidden]. */
+ * common shape.  Needs hidden 2048, inter 512, top_k <= 8 (plus an optional
+ * shared expert) and experts <= 256; rmoe_chain_table_pack checks the
+ * shape without touching the device.  x, out bf16 [hidden]. */
 size_t rmoe_chain_table_bytes(int32_t n_layers);
 int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers,
                           void* host_table);

@@ -512,6 +512,8 @@ void orc_route_token(const orc_layer* L, const uint16_t* x, int32_t* idx,
     pb[j] = round_bf16(expf(logit[idx[j]] - m) / z);
     total += pb[j];
   }
+  /* mlx-lm divides by scores.sum(-1), a bf16 value */
+  total = round_bf16(total);
   for (int j = 0; j < K; ++j)
     scores[j] = L->norm_topk_prob ? round_bf16(pb[j] / total) : pb[j];
 }

@@ -48,8 +48,9 @@ exact bf16 rounding points inside ``gather_qmm`` and the tie order of
   north-star tolerance instead.
 * ``block_forward(mode="contract")`` is the HIP kernels' contract: fp32/f64
   arithmetic with bf16 rounding of x_up, x_gate, the SwiGLU activation, each
-  expert's down output, the router probabilities/scores, the shared gate and
-  the block output.  ``mode="mlx"`` adds the extra bf16 roundings an
+  expert's down output, the router probabilities, the renormalisation
+  denominator (mlx-lm's ``scores.sum(-1)`` of bf16 scores is bf16), the
+  scores, the shared gate and the block output.  ``mode="mlx"`` adds the extra bf16 roundings an
   op-by-op mlx-lm evaluation performs (silu output, score products, the
   routed sum, the gated shared term)
   (max-abs <= 2e-2, cosine >= 0.9999) is checked against it.
@@ -357,6 +358,16 @@ def route(x_bits, router_w_bits, top_k, norm_topk_prob=True):
     [1, E, H])."""
     logits = round_bf16(gate_logits(x_bits, router_w_bits))
     idx = topk_rank(logits, top_k)
+    return idx, selected_scores(logits, idx, norm_topk_prob), logits
+
+
+def selected_scores(logits, idx, norm_topk_prob=True):
+    """Scores of the selected experts ``idx`` [T, k] from bf16-valued logits
+    [T, E]: softmax in fp32 over every expert (sequential sum), probabilities
+    rounded to bf16 (mlx's softmax of bf16 logits returns bf16), and with
+    ``norm_topk_prob`` divided by ``scores.sum(-1)``, which mlx-lm computes on
+    bf16 scores and so rounds to bf16 (fp32 sum in slot order, then bf16);
+    the quotient is bf16."""
     m = logits.max(axis=-1, keepdims=True)
     e = np.exp((logits - m).astype(np.float32)).astype(np.float32)
     z = np.zeros(e.shape[0], dtype=np.float32)
@@ -364,14 +375,12 @@ def route(x_bits, router_w_bits, top_k, norm_topk_prob=True):
         z = (z + e[:, i]).astype(np.float32)
     p = (e / z[:, None]).astype(np.float32)
     pb = round_bf16(np.take_along_axis(p, idx, axis=-1))
-    if norm_topk_prob:
-        tot = np.zeros(pb.shape[0], dtype=np.float32)
-        for j in range(top_k):
-            tot = (tot + pb[:, j]).astype(np.float32)
-        scores = round_bf16(pb / tot[:, None])
-    else:
-        scores = pb
-    return idx, scores.astype(np.float32), logits
+    if not norm_topk_prob:
+        return pb.astype(np.float32)
+    tot = np.zeros(pb.shape[0], dtype=np.float32)
+    for j in range(idx.shape[1]):
+        tot = (tot + pb[:, j]).astype(np.float32)
+    return round_bf16(pb / round_bf16(tot)[:, None]).astype(np.float32)
 
 
 # --------------------------------------------------------------------------
@@ -487,18 +496,8 @@ def block_forward(layer: Layer, x_bits: np.ndarray, residual_bits=None,
     if idx is None:
         idx = r_idx
     else:
-        # recompute scores for the forced selection
-        m = logits.max(axis=-1, keepdims=True)
-        e = np.exp((logits - m).astype(np.float32)).astype(np.float32)
-        z = np.zeros(e.shape[0], dtype=np.float32)
-        for i in range(e.shape[1]):
-            z = (z + e[:, i]).astype(np.float32)
-        p = (e / z[:, None]).astype(np.float32)
-        pb = round_bf16(np.take_along_axis(p, idx, axis=-1))
-        tot = np.zeros(pb.shape[0], dtype=np.float32)
-        for j in range(layer.top_k):
-            tot = (tot + pb[:, j]).astype(np.float32)
-        scores = round_bf16(pb / tot[:, None]) if layer.norm_topk_prob else pb
+        # scores of the forced selection
+        scores = selected_scores(logits, idx, layer.norm_topk_prob)
     y = switch_glu(layer, x_bits, idx, mode)
     T = x_bits.shape[0]
     if mode == "mlx":

@@ -20,6 +20,7 @@ RMOE_EALIGN = -3
 RMOE_EWS = -4
 RMOE_EHIP = -5
 RMOE_ENULL = -6
+RMOE_ETIMEOUT = -7
 
 ABI_VERSION = 3
 

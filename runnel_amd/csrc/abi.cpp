@@ -90,6 +90,16 @@ int check_down_width(int inter, int bits, const char* name) {
   return RMOE_OK;
 }
 
+// The few-token gate/up kernel gives each lane at most kMaxGateUpChunksPerLane
+// 16-byte chunks of a row: hidden <= 256 chunks (4096 at 8 bits, 8192 at 4).
+int check_hidden_width(int hidden, int bits, const char* name) {
+  const int max_h = 64 * rmoe::kMaxGateUpChunksPerLane * values_per_chunk(bits);
+  if (hidden > max_h)
+    return fail(RMOE_EINVAL, "%s: hidden %d too large at %d bits (at most %d)", name, hidden,
+                bits, max_h);
+  return RMOE_OK;
+}
+
 int check_layer(const rmoe_layer* L) {
   if (!L) return fail(RMOE_ENULL, "layer is NULL");
   if (L->hidden < 64 || L->hidden % 64)
@@ -125,6 +135,7 @@ int check_layer(const rmoe_layer* L) {
   if (L->gate_up.bits != L->down.bits)
     return fail(RMOE_EBITS, "gate_up and down must share one bit width");
   if ((rc = check_down_width(L->inter, L->down.bits, "down"))) return rc;
+  if ((rc = check_hidden_width(L->hidden, L->gate_up.bits, "gate_up"))) return rc;
   const bool has_shared = L->shared_gate_up.w != nullptr;
   if (has_shared) {
     if ((rc = check_qweight(&L->shared_gate_up, "shared_gate_up"))) return rc;
@@ -325,13 +336,20 @@ rmoe::DecodeArgs decode_args(const rmoe_layer* L, const uint16_t* x, int T,
   return a;
 }
 
-// The single-launch decode kernel is specialised for the block's native
-// shape and needs one resident workgroup per CU with enough waves to give
-// every down row its own wave.
+// Shape part of the single-launch decode kernel's eligibility (host only):
+// the block's native shape, at most kMaxFusedRouted routed slots (the
+// kernel ranks that many) plus the shared expert, and at most
+// kFusedMaxExperts experts (four ranking keys per lane).
+bool fused_shape_ok(const rmoe_layer* L) {
+  return L->hidden == rmoe::kFusedH && L->inter == rmoe::kFusedI &&
+         L->top_k <= rmoe::kMaxFusedRouted && L->experts <= rmoe::kFusedMaxExperts;
+}
+
+// The single-launch decode kernel also needs one resident workgroup per CU
+// with enough waves to give every down row its own wave.
 bool fused_eligible(const rmoe_layer* L, int* grid) {
+  if (!fused_shape_ok(L)) return false;
   const int units = L->top_k + (L->shared_gate_up.w ? 1 : 0);
-  if (L->hidden != rmoe::kFusedH || L->inter != rmoe::kFusedI) return false;
-  if (units > rmoe::kMaxFusedUnits || L->experts > rmoe::kFusedMaxExperts) return false;
   int g = 0;
   if (rmoe::fused_grid(L->gate_up.bits, router_quantized(L), L->post_norm_w != nullptr, &g) !=
       hipSuccess)
@@ -396,6 +414,7 @@ int check_switch(const rmoe_qweight* gate_up, const rmoe_qweight* down, int32_t 
   if (down->bits != gate_up->bits)
     return fail(RMOE_EBITS, "gate_up and down must share one bit width");
   if ((rc = check_down_width(I, down->bits, "down"))) return rc;
+  if ((rc = check_hidden_width(H, gate_up->bits, "gate_up"))) return rc;
   if (top_k < 1 || top_k > rmoe::kMaxTopK)
     return fail(RMOE_EINVAL, "top_k must be in [1, %d] (got %d)", rmoe::kMaxTopK, top_k);
   return RMOE_OK;
@@ -485,6 +504,7 @@ const char* rmoe_status_string(int status) {
     case RMOE_EWS: return "workspace too small";
     case RMOE_EHIP: return "HIP runtime error";
     case RMOE_ENULL: return "NULL pointer";
+    case RMOE_ETIMEOUT: return "single-launch decode timed out (outputs not valid)";
     default: return "unknown status";
   }
 }
@@ -795,15 +815,17 @@ int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers, void* host
         (b.post_norm_w == nullptr) != (a.post_norm_w == nullptr))
       return fail(RMOE_EINVAL, "layer %d differs in shape or format from layer 0", i);
   }
-  for (int i = 0; i < n_layers; ++i) {
-    const rmoe_layer& b = layers[i];
-    if (!fused_eligible(&b, &grid))
-      return fail(RMOE_EINVAL,
-                  "chained decode needs hidden %d, inter %d, top_k + shared <= %d, "
-                  "experts <= %d and one resident workgroup per CU",
-                  rmoe::kFusedH, rmoe::kFusedI, rmoe::kMaxFusedUnits, rmoe::kFusedMaxExperts);
-    static_cast<rmoe::FusedLayer*>(host_table)[i] = fused_layer(&b);
-  }
+  // the shape first: it needs no device, so argument errors never depend on one
+  if (!fused_shape_ok(&layers[0]))
+    return fail(RMOE_EINVAL,
+                "chained decode needs hidden %d, inter %d, top_k <= %d (plus the shared "
+                "expert) and experts <= %d (got %d, %d, %d, %d)",
+                rmoe::kFusedH, rmoe::kFusedI, rmoe::kMaxFusedRouted, rmoe::kFusedMaxExperts,
+                layers[0].hidden, layers[0].inter, layers[0].top_k, layers[0].experts);
+  if (!fused_eligible(&layers[0], &grid))
+    return fail(RMOE_EINVAL, "chained decode needs one resident workgroup per CU");
+  for (int i = 0; i < n_layers; ++i)
+    static_cast<rmoe::FusedLayer*>(host_table)[i] = fused_layer(&layers[i]);
   return ok();
 }
 

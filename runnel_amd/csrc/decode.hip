@@ -47,7 +47,8 @@ __device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const f
   float total = 0.0f;
   for (int j = 0; j < p.K; ++j)
     total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
-  const float score = p.norm ? round_bf16(pb / total) : pb;
+  // the denominator is bf16, as mlx-lm's scores.sum(-1) of bf16 scores
+  const float score = p.norm ? round_bf16(pb / round_bf16(total)) : pb;
   if (lane < p.K) {
     p.idx[t * p.K + lane] = my_sel;
     p.scores[t * (p.K + 1) + lane] = score;

@@ -575,7 +575,8 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         if (j < K) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
       if (lane < K) {
         const int e = (int)(0xFFFFu - (my & 0xFFFFu));
-        const float score = p.norm ? round_bf16(pb / total) : pb;
+        // bf16 denominator, as mlx-lm's scores.sum(-1) of bf16 scores
+        const float score = p.norm ? round_bf16(pb / round_bf16(total)) : pb;
         s_idx[lane] = e;
         s_coef[lane] = score;
         if (wg == 0 && last && p.idx_out) {

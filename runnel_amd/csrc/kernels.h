@@ -14,6 +14,7 @@ constexpr int kUnitBatch = 9;      // down kernel: loads in flight per lane
 constexpr int kMaxTokens = 65535;  // grid.y of the router; counters reserved
 constexpr int kRouterBatch = 4;    // router: 16-byte loads in flight per lane
 constexpr int kStageBatch = 8;     // down: float4 act loads in flight per lane
+constexpr int kMaxGateUpChunksPerLane = 4;  // gate_up_kernel: 256 chunks per row
 
 struct QW {
   const uint32_t* w;
@@ -59,7 +60,8 @@ struct QmvArgs {
 // ---- single-launch decode (fused.hip): one token, one or more layers.
 constexpr int kFusedThreads = 512;          // 8 waves, one workgroup per CU
 constexpr int kFusedMaxGrid = 1024;
-constexpr int kMaxFusedUnits = 9;           // top-k <= 8 plus the shared expert
+constexpr int kMaxFusedRouted = 8;          // routed slots the kernel ranks
+constexpr int kMaxFusedUnits = kMaxFusedRouted + 1;  // plus the shared expert
 constexpr int kMaxFusedPairsPerWave = 3;
 constexpr int kMaxFusedRowsPerWave = 1;
 constexpr int kFusedMaxExperts = 256;

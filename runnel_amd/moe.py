@@ -228,6 +228,16 @@ class SparseMoeBlock(nn.Module):
             return out.reshape(*lead, D)
         return self._composed(x, residual)
 
+    def check_status(self, device="cuda") -> None:
+        """Raise RmoeError(RMOE_ETIMEOUT) if a single-launch decode made by
+        this block's calls on `device` (current stream) gave up a
+        cross-workgroup wait, clearing the sticky word first.  Eager calls
+        with plain launches check by themselves; graph users call this after
+        a replay (it synchronises)."""
+        ws = native.default_workspace(device, "block")
+        if ws is not None:
+            native.check_status(ws)
+
     def _composed(self, x, residual):
         """Module-by-module evaluation for unfused or non-SwiGLU layers."""
         D = x.shape[-1]
@@ -263,6 +273,9 @@ class PostAttentionMoE(nn.Module):
 
     def layer_handle(self) -> native.LayerHandle | None:
         return self.mlp.layer_handle(self.post_attention_layernorm)
+
+    def check_status(self, device="cuda") -> None:
+        self.mlp.check_status(device)
 
     def __call__(self, h: torch.Tensor) -> torch.Tensor:
         D = h.shape[-1]

@@ -24,6 +24,28 @@ def _require_cuda(*tensors):
             raise ValueError("runnel_amd kernels take GPU tensors")
 
 
+def _check_rows(t: torch.Tensor, name: str, rows: int, cols: int) -> None:
+    """t must be a bf16 [rows, cols] tensor (checked before any pointer
+    reaches the library, which trusts the shapes it is given)."""
+    if t.dtype != BF16:
+        raise ValueError(f"{name} must be bfloat16 (got {t.dtype})")
+    if t.dim() != 2 or tuple(t.shape) != (rows, cols):
+        raise ValueError(f"{name} must be [{rows}, {cols}] (got {list(t.shape)})")
+
+
+def _check_out(out: torch.Tensor, rows: int, cols: int) -> None:
+    _check_rows(out, "out", rows, cols)
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+
+
+def _check_x(x: torch.Tensor, cols: int) -> None:
+    if x.dtype != BF16 or x.dim() != 2:
+        raise ValueError("x must be a 2-D bfloat16 tensor")
+    if x.shape[1] != cols:
+        raise ValueError(f"x must be [tokens, {cols}] (got {list(x.shape)})")
+
+
 def values_per_word(bits: int) -> int:
     if bits not in (4, 8):
         raise ValueError(f"bits must be 4 or 8 (got {bits})")
@@ -44,6 +66,7 @@ def qweight_struct(weight, scales, biases, bits: int, group_size: int = 64) -> _
             raise ValueError(f"{name} is required")
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
+    _require_cuda(weight, scales, biases)
     if weight.dtype not in (torch.int32, getattr(torch, "uint32", torch.int32)):
         raise ValueError("packed weight must be int32/uint32")
     if scales.dtype != BF16 or biases.dtype != BF16:
@@ -63,6 +86,10 @@ class Workspace:
 
     def __init__(self):
         self._bufs: dict = {}
+
+    def peek(self, device, key: str = "default") -> torch.Tensor | None:
+        device = torch.device(device)
+        return self._bufs.get((str(device), torch.cuda.current_stream(device).cuda_stream, key))
 
     def get(self, device, nbytes: int, key: str = "default") -> torch.Tensor:
         k = (str(device), torch.cuda.current_stream(device).cuda_stream, key)
@@ -87,9 +114,12 @@ def gather_qmm(x: torch.Tensor, weight, scales, biases, bits: int, group_size: i
     x: bf16 [x_rows, K]; rhs_indices / lhs_indices: int32 [M] (None: expert
     0 / row m).  Returns [M, N] in bf16 or float32."""
     lib = _lib.load()
-    _require_cuda(x, weight, rhs_indices, lhs_indices)
     if x.dtype != BF16 or x.dim() != 2:
         raise ValueError("x must be a 2-D bfloat16 tensor")
+    cols = weight.shape[-1] * values_per_word(bits)
+    if x.shape[1] != cols:
+        raise ValueError(f"x has {x.shape[1]} columns, the weight {cols}")
+    _require_cuda(x, weight, rhs_indices, lhs_indices)
     x = x.contiguous()
     qw = qweight_struct(weight, scales, biases, bits, group_size)
     if lhs_indices is not None:
@@ -121,11 +151,14 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, gate_up: _lib.QWeight,
     """Packed [up; gate] projection + SwiGLU + down per (token, slot):
     x bf16 [T, H], indices int [T, k] -> bf16 [T, k, H] (uncombined)."""
     lib = _lib.load()
+    if indices.dim() != 2:
+        raise ValueError("indices must be [tokens, k]")
+    T, k = indices.shape
+    H = gate_up.cols
+    _check_rows(x, "x", T, H)
     _require_cuda(x, indices)
     x = x.contiguous()
     idx = indices.to(torch.int32).contiguous()
-    T, k = idx.shape
-    H = gate_up.cols
     y = torch.empty((T, k, H), dtype=BF16, device=x.device)
     need = lib.rmoe_switch_workspace_bytes(ctypes.byref(gate_up), ctypes.byref(down), T, k)
     ws = WORKSPACE.get(x.device, need, "switch")
@@ -143,14 +176,20 @@ def switch_combine(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor
     indices int [T, k], weights float32 [T, k] -> bf16 [T, H] =
     bf16(sum_j weights[t, j] * y[t, j]) (+ residual)."""
     lib = _lib.load()
+    if indices.dim() != 2:
+        raise ValueError("indices must be [tokens, k]")
+    T, k = indices.shape
+    H = gate_up.cols
+    _check_rows(x, "x", T, H)
+    if tuple(weights.shape) != (T, k):
+        raise ValueError(f"weights must be [{T}, {k}] (got {list(weights.shape)})")
+    if residual is not None:
+        _check_rows(residual, "residual", T, H)
     _require_cuda(x, indices, weights, residual)
     x = x.contiguous()
     idx = indices.to(torch.int32).contiguous()
     w = weights.to(torch.float32).contiguous()
-    T, k = idx.shape
-    if tuple(w.shape) != (T, k):
-        raise ValueError(f"weights must be [{T}, {k}] (got {list(w.shape)})")
-    out = torch.empty((T, gate_up.cols), dtype=BF16, device=x.device)
+    out = torch.empty((T, H), dtype=BF16, device=x.device)
     res = None if residual is None else residual.contiguous()
     need = lib.rmoe_switch_combine_workspace_bytes(ctypes.byref(gate_up), ctypes.byref(down),
                                                    T, k)
@@ -226,17 +265,22 @@ def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
             shared_gate_w = shared_gate_w.reshape(-1).contiguous()
             keep.append(shared_gate_w)
     if router_w is not None:
-        if router_w.dtype != BF16 or not router_w.is_contiguous():
+        if (router_w.dtype != BF16 or not router_w.is_contiguous()
+                or router_w.dim() != 2):
             raise ValueError("router weight must be contiguous bfloat16 [experts, hidden]")
         keep.append(router_w)
         E, H = router_w.shape
     else:
         E, H = rq.rows, rq.cols
+    if shared_gate_w is not None and (shared_gate_w.dtype != BF16
+                                      or shared_gate_w.numel() != H):
+        raise ValueError(f"shared gate must be bfloat16 [{H}]")
     if post_norm_w is not None:
         post_norm_w = post_norm_w.reshape(-1).contiguous()
         if post_norm_w.dtype != BF16 or post_norm_w.numel() != H:
             raise ValueError(f"post_norm_w must be bfloat16 [{H}]")
         keep.append(post_norm_w)
+    _require_cuda(router_w, shared_gate_w, post_norm_w)
     s = _lib.Layer(H, gu.rows // 2, shared_inter, E, top_k, int(bool(norm_topk_prob)),
                    _lib.ptr(router_w), _lib.ptr(shared_gate_w), gu, dn, sgu, sdn, rq, sgq,
                    _lib.ptr(post_norm_w), float(norm_eps))
@@ -247,14 +291,28 @@ def make_layer(router_w, gate_up, down, top_k: int, norm_topk_prob: bool = True,
 
 def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None = None,
               out: torch.Tensor | None = None, return_routing: bool = False,
-              workspace: torch.Tensor | None = None):
-    """Whole SparseMoeBlock on x bf16 [T, H] -> bf16 [T, H]."""
+              workspace: torch.Tensor | None = None, check: bool | None = None):
+    """Whole SparseMoeBlock on x bf16 [T, H] -> bf16 [T, H].
+
+    ``check``: read (and clear) the workspace's status word after the call
+    and raise RmoeError(RMOE_ETIMEOUT) if a cross-workgroup wait of the
+    single-launch decode gave up; this synchronises the stream.  None (the
+    default) checks one-token calls made with plain launches
+    (``set_cooperative_launch(False)``) outside graph capture, the only
+    eager calls whose waits can give up; graph users call ``check_status``
+    on the workspace after a replay."""
     lib = _lib.load()
-    _require_cuda(x, residual, out)
-    if x.dtype != BF16 or x.dim() != 2:
-        raise ValueError("x must be a 2-D bfloat16 tensor")
-    x = x.contiguous()
+    H = layer.hidden
+    _check_x(x, H)
     T = x.shape[0]
+    if residual is not None:
+        _check_rows(residual, "residual", T, H)
+    if out is not None:
+        _check_out(out, T, H)
+    _require_cuda(x, residual, out)
+    x = x.contiguous()
+    if residual is not None:
+        residual = residual.contiguous()
     if out is None:
         out = torch.empty_like(x)
     idx = scores = None
@@ -263,10 +321,14 @@ def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None
         scores = torch.empty((T, layer.top_k), dtype=torch.float32, device=x.device)
     need = layer.workspace_bytes(T)
     ws = workspace if workspace is not None else WORKSPACE.get(x.device, need, "block")
+    if check is None:
+        check = T == 1 and not _COOPERATIVE[0] and not _capturing(x.device)
     _lib.check(lib.rmoe_moe_block(ctypes.byref(layer.struct), x.data_ptr(), T,
                                   _lib.ptr(residual), out.data_ptr(), _lib.ptr(idx),
                                   _lib.ptr(scores), ws.data_ptr(), ws.numel(),
                                   _lib.stream_handle(x.device)))
+    if check:
+        check_status(ws)
     if return_routing:
         return out, idx, scores
     return out
@@ -294,34 +356,81 @@ class Chain:
 
 
 def moe_chain(chain: Chain, x: torch.Tensor, out: torch.Tensor | None = None,
-              workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """One token x bf16 [1, H] (or [H]) through every layer of the chain."""
+              workspace: torch.Tensor | None = None,
+              check: bool | None = None) -> torch.Tensor:
+    """One token x bf16 [1, H] (or [H]) through every layer of the chain.
+    ``check`` as for ``moe_block`` (None: check plain eager launches)."""
     lib = _lib.load()
-    _require_cuda(x)
+    H = chain.layers[0].hidden
+    if x.dtype != BF16 or x.numel() != H or x.dim() not in (1, 2):
+        raise ValueError(f"x must be bfloat16 [1, {H}] or [{H}] (got {list(x.shape)})")
+    if out is not None and (out.dtype != BF16 or out.shape != x.shape
+                            or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous bfloat16 tensor of shape {list(x.shape)}")
+    _require_cuda(x, out)
     x = x.contiguous()
     if out is None:
         out = torch.empty_like(x)
     ws = workspace if workspace is not None else WORKSPACE.get(
         x.device, chain.workspace_bytes(), "block")
+    if check is None:
+        check = not _COOPERATIVE[0] and not _capturing(x.device)
     _lib.check(lib.rmoe_moe_chain(ctypes.byref(chain.layers[0].struct), chain.table.data_ptr(),
                                   chain.n, x.data_ptr(), out.data_ptr(), ws.data_ptr(),
                                   ws.numel(), _lib.stream_handle(x.device)))
+    if check:
+        check_status(ws)
     return out
+
+
+# The launch mode last set through set_cooperative_launch (the library's
+# default is cooperative).
+_COOPERATIVE = [True]
+
+
+def _capturing(device) -> bool:
+    return torch.cuda.is_current_stream_capturing()
 
 
 def set_cooperative_launch(enabled: bool) -> bool:
     """Launch mode of the single-launch decode kernel outside graph capture
     (process-wide; returns the previous mode).  False: plain launches, which
     overlap the previous call (about 17 us less per eager call) and are
-    valid while nothing else runs on the device during the call."""
-    return bool(_lib.load().rmoe_set_cooperative_launch(1 if enabled else 0))
+    valid while nothing else runs on the device during the call; moe_block
+    and moe_chain then check the status word after each one-token call
+    unless told not to."""
+    prev = bool(_lib.load().rmoe_set_cooperative_launch(1 if enabled else 0))
+    _COOPERATIVE[0] = bool(enabled)
+    return prev
 
 
-def workspace_status(ws: torch.Tensor) -> int:
+def workspace_status(ws: torch.Tensor, clear: bool = False) -> int:
     """The status word of a workspace (nonzero: a single-launch decode timed
-    out waiting for another workgroup)."""
+    out waiting for another workgroup, and that call's outputs are not
+    valid).  The word is sticky: every later call leaves it set until it is
+    cleared.  Reading it synchronises with the work queued on ws's device."""
     off = _lib.load().rmoe_workspace_status_offset()
-    return int(ws[off:off + 4].view(torch.int32).item())
+    word = ws[off:off + 4].view(torch.int32)
+    v = int(word.item())
+    if clear and v:
+        word.zero_()
+    return v
+
+
+def check_status(ws: torch.Tensor) -> None:
+    """Raise RmoeError(RMOE_ETIMEOUT) if the workspace's status word is set,
+    clearing it first (graph users call this after a replay)."""
+    if workspace_status(ws, clear=True):
+        raise _lib.RmoeError(_lib.RMOE_ETIMEOUT,
+                             "a single-launch decode timed out waiting for another "
+                             "workgroup; its outputs are not valid")
+
+
+def default_workspace(device, key: str = "block") -> torch.Tensor | None:
+    """The library-managed workspace that calls without an explicit
+    workspace use on `device` and the current stream (None before the
+    first such call)."""
+    return WORKSPACE.peek(device, key)
 
 
 def router(router_w, x: torch.Tensor, top_k: int, norm_topk_prob: bool = True):
@@ -329,10 +438,14 @@ def router(router_w, x: torch.Tensor, top_k: int, norm_topk_prob: bool = True):
     (weight, scales, biases) triple of an 8-bit group-64 quantized gate ->
     (indices int32 [T, k] in rank order, scores float32 [T, k])."""
     lib = _lib.load()
-    x = x.contiguous()
+    if x.dtype != BF16 or x.dim() != 2:
+        raise ValueError("x must be a 2-D bfloat16 tensor")
     T, H = x.shape
     w, rq, keep = _gate(router_w, None, "router gate")
+    if w is not None and (w.dim() != 2 or w.shape[1] != H):
+        raise ValueError(f"router gate must be [experts, {H}] (got {list(w.shape)})")
     _require_cuda(x, w, *keep)
+    x = x.contiguous()
     E = rq.rows if w is None else w.shape[0]
     idx = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     scores = torch.empty((T, top_k), dtype=torch.float32, device=x.device)

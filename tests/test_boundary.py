@@ -412,3 +412,121 @@ def test_cooperative_launch_switch_returns_previous_mode():
     assert lib.rmoe_set_cooperative_launch(0) == 1
     assert lib.rmoe_set_cooperative_launch(7) == 0   # any nonzero turns it on
     assert lib.rmoe_set_cooperative_launch(1) == 1
+
+
+def test_single_launch_shape_rejects_nine_routed_slots():
+    """The single-launch kernel ranks at most 8 routed slots: a top-9 layer
+    without a shared expert is refused by the chained decode on the host
+    (the shape check needs no device), and a one-token block call of it takes
+    the multi-kernel path instead."""
+    lib = _lib.load()
+    n = lib.rmoe_chain_table_bytes(1)
+    buf = (ctypes.c_uint8 * n)()
+    top9 = (_lib.Layer * 1)(_layer(H=2048, I=512, E=16, K=9, shared=False))
+    assert lib.rmoe_validate_layer(top9) == _lib.RMOE_OK
+    assert lib.rmoe_chain_table_pack(top9, 1, ctypes.addressof(buf)) == _lib.RMOE_EINVAL
+    assert b"top_k <= 8" in lib.rmoe_last_error()
+    big = (_lib.Layer * 1)(_layer(H=2048, I=512, E=257, K=8))
+    assert lib.rmoe_chain_table_pack(big, 1, ctypes.addressof(buf)) == _lib.RMOE_EINVAL
+    assert b"experts <= 256" in lib.rmoe_last_error()
+
+
+def test_hidden_limit_of_the_few_token_gate_up_kernel():
+    """The few-token gate/up kernel covers 256 16-byte chunks per row:
+    hidden <= 4096 at 8 bits and <= 8192 at 4 bits; wider layers are refused
+    before anything is launched rather than silently truncated."""
+    lib = _lib.load()
+    for bits, ok_h in ((8, 4096), (4, 8192)):
+        assert lib.rmoe_validate_layer(ctypes.byref(_layer(bits=bits, H=ok_h))) == _lib.RMOE_OK
+        rc = lib.rmoe_validate_layer(ctypes.byref(_layer(bits=bits, H=ok_h + 64)))
+        assert rc == _lib.RMOE_EINVAL
+        assert b"too large" in lib.rmoe_last_error()
+    gu, dn = _qw(8, 4, 128, 4160), _qw(8, 4, 4160, 64)
+    need = lib.rmoe_switch_workspace_bytes(ctypes.byref(gu), ctypes.byref(dn), 2, 2)
+    assert lib.rmoe_switch_glu(ctypes.byref(gu), ctypes.byref(dn), FAKE, 2, FAKE, 2, FAKE,
+                               FAKE, need, None) == _lib.RMOE_EINVAL
+
+
+def _host_handle(H=256):
+    from runnel_amd import native
+    return native.LayerHandle(_layer(H=H), ())
+
+
+def test_python_block_checks_shapes_before_the_library():
+    """x, residual and out are checked against [tokens, hidden] (and out for
+    dtype and contiguity) before any pointer is handed over: the library
+    trusts the shapes it is given."""
+    from runnel_amd import native
+    h = _host_handle(256)
+    bf = torch.bfloat16
+    with pytest.raises(ValueError, match=r"x must be \[tokens, 256\]"):
+        native.moe_block(h, torch.zeros(2, 128, dtype=bf))
+    with pytest.raises(ValueError, match="x must be a 2-D bfloat16"):
+        native.moe_block(h, torch.zeros(2, 256, dtype=torch.float32))
+    x = torch.zeros(2, 256, dtype=bf)
+    with pytest.raises(ValueError, match=r"residual must be \[2, 256\]"):
+        native.moe_block(h, x, residual=torch.zeros(2, 128, dtype=bf))
+    with pytest.raises(ValueError, match="residual must be bfloat16"):
+        native.moe_block(h, x, residual=torch.zeros(2, 256))
+    with pytest.raises(ValueError, match="out must be bfloat16"):
+        native.moe_block(h, x, out=torch.zeros(2, 256, dtype=torch.float16))
+    with pytest.raises(ValueError, match=r"out must be \[2, 256\]"):
+        native.moe_block(h, x, out=torch.zeros(1, 256, dtype=bf))
+    with pytest.raises(ValueError, match="out must be contiguous"):
+        native.moe_block(h, x, out=torch.zeros(256, 2, dtype=bf).t())
+    # well-formed host tensors get as far as the device check
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.moe_block(h, x, residual=torch.zeros(4, 256, dtype=bf)[::2])
+
+
+def test_python_switch_and_qmm_check_shapes_before_the_library():
+    from runnel_amd import native
+    bf = torch.bfloat16
+    gu, dn = _qw(8, 4, 128, 256), _qw(8, 4, 256, 64)
+    idx = torch.zeros(2, 2, dtype=torch.int32)
+    with pytest.raises(ValueError, match=r"x must be \[2, 256\]"):
+        native.switch_glu(torch.zeros(2, 128, dtype=bf), idx, gu, dn)
+    with pytest.raises(ValueError, match=r"x must be \[2, 256\]"):
+        native.switch_combine(torch.zeros(3, 256, dtype=bf), idx, torch.zeros(2, 2), gu, dn)
+    with pytest.raises(ValueError, match=r"weights must be \[2, 2\]"):
+        native.switch_combine(torch.zeros(2, 256, dtype=bf), idx, torch.zeros(2, 3), gu, dn)
+    with pytest.raises(ValueError, match=r"residual must be \[2, 256\]"):
+        native.switch_combine(torch.zeros(2, 256, dtype=bf), idx, torch.zeros(2, 2), gu, dn,
+                              residual=torch.zeros(2, 255, dtype=bf))
+    w = torch.zeros(1, 32, 32, dtype=torch.int32)   # 128 columns at 8 bits
+    s = torch.zeros(1, 32, 2, dtype=bf)
+    with pytest.raises(ValueError, match="x has 256 columns, the weight 128"):
+        native.gather_qmm(torch.zeros(1, 256, dtype=bf), w, s, s, 8)
+
+
+def test_layer_weights_must_live_on_the_gpu():
+    from runnel_amd import native
+    bf = torch.bfloat16
+    bank = (torch.zeros(4, 128, 64, dtype=torch.int32), torch.zeros(4, 128, 4, dtype=bf),
+            torch.zeros(4, 128, 4, dtype=bf))
+    dbank = (torch.zeros(4, 256, 16, dtype=torch.int32), torch.zeros(4, 256, 1, dtype=bf),
+             torch.zeros(4, 256, 1, dtype=bf))
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.make_layer(torch.zeros(4, 256, dtype=bf), bank, dbank, 2)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        native.qweight_struct(*bank, 8)
+
+
+def test_status_word_is_read_cleared_and_raised():
+    """check_status raises RmoeError(RMOE_ETIMEOUT) once for a set (sticky)
+    status word and clears it; workspace_status reads it without clearing
+    unless asked."""
+    from runnel_amd import native
+    lib = _lib.load()
+    off = lib.rmoe_workspace_status_offset()
+    ws = torch.zeros(off + 256, dtype=torch.uint8)
+    native.check_status(ws)                       # clear: nothing raised
+    ws[off:off + 4].view(torch.int32).fill_(1)
+    assert native.workspace_status(ws) == 1
+    assert native.workspace_status(ws) == 1       # reading does not clear
+    with pytest.raises(_lib.RmoeError) as e:
+        native.check_status(ws)
+    assert e.value.status == _lib.RMOE_ETIMEOUT
+    assert native.workspace_status(ws) == 0
+    native.check_status(ws)
+    assert b"timed out" in lib.rmoe_status_string(_lib.RMOE_ETIMEOUT)

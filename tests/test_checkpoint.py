@@ -160,10 +160,11 @@ def write_checkpoint(root: Path, L: M.Layer, layer: int = 0, bits: int = 8, extr
 
 @pytest.mark.parametrize("router_bits", [None, 8])
 @pytest.mark.parametrize("bits", [8, 4])
-def test_load_moe_block_from_checkpoint(tmp_path, bits, router_bits):
+def test_load_moe_block_from_checkpoint(tmp_path, monkeypatch, bits, router_bits):
     """Every buffer equals the checkpoint's bytes, gate/up are packed
     [up; gate], the gates take the format the checkpoint has, and the C ABI
-    accepts the layer it describes."""
+    accepts the layer it describes (host tensors are refused for the kernels;
+    the device check is lifted to describe them here)."""
     from runnel_amd import FusedQuantizedSwitchGLU, Linear, QuantizedLinear
     L = M.make_layer(3, hidden=256, inter=128, experts=8, top_k=2, bits=bits,
                      router_bits=router_bits)
@@ -182,13 +183,18 @@ def test_load_moe_block_from_checkpoint(tmp_path, bits, router_bits):
         assert np.array_equal(blk.gate.weight.numpy().view(np.uint32), L.router_w.w[0])
     se = blk.shared_expert
     assert np.array_equal(se.down_proj.weight.numpy().view(np.uint32), L.shared_down.w[0])
+    with pytest.raises(ValueError, match="GPU tensors"):
+        blk.layer_handle()
+    from runnel_amd import native
+    monkeypatch.setattr(native, "_require_cuda", lambda *t: None)
     h = blk.layer_handle()
     assert h is not None and h.struct.experts == 8 and h.struct.hidden == 256
     assert (h.struct.router_q.w is not None) == (router_bits is not None)
 
 
-def test_load_decoder_moe_reads_the_post_attention_norm(tmp_path):
-    from runnel_amd import PostAttentionMoE
+def test_load_decoder_moe_reads_the_post_attention_norm(tmp_path, monkeypatch):
+    from runnel_amd import PostAttentionMoE, native
+    monkeypatch.setattr(native, "_require_cuda", lambda *t: None)  # describe host tensors
     L = M.make_layer(5, hidden=256, inter=128, experts=8, top_k=2, bits=8)
     nw = M.f32_to_bf16(np.linspace(0.5, 1.5, 256).astype(np.float32))
     write_checkpoint(tmp_path, L, layer=1,

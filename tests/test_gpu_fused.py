@@ -235,3 +235,30 @@ def test_plain_eager_launch_equals_cooperative(torch_cuda):
     assert native.workspace_status(ws) == 0
     for a, b in zip(coop, plain):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_one_token_top9_without_shared_expert(torch_cuda, bits):
+    """A layer of the decode shape with nine routed slots and no shared
+    expert: the single-launch kernel ranks at most eight, so a one-token
+    call takes the router / gate-up / down kernels and matches the oracle
+    (routing exact, every index inside the bank)."""
+    torch = torch_cuda
+    from runnel_amd import native
+    from helpers import layer_to_dev
+    L = M.make_layer(7900 + bits, hidden=2048, inter=512, experts=16, top_k=9, bits=bits,
+                     shared=False)
+    h = layer_to_dev(L)
+    xs = M.make_x(7901, 3, 2048)
+    outs, idxs = [], []
+    for t in range(3):
+        o, i, _ = native.moe_block(h, dev_bf16(xs[t:t + 1]), return_routing=True)
+        outs.append(host_bf16(o))
+        idxs.append(i.cpu().numpy())
+    torch.cuda.synchronize()
+    ref, ref_idx, _ = M.block_forward(L, xs)
+    gidx = np.concatenate(idxs)
+    assert gidx.min() >= 0 and gidx.max() < 16
+    assert np.array_equal(gidx, ref_idx)
+    got = np.concatenate(outs)
+    assert _contract_mismatches(got, ref) <= got.size // 500
