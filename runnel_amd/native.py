@@ -87,12 +87,18 @@ class Workspace:
     def __init__(self):
         self._bufs: dict = {}
 
+    @staticmethod
+    def _key(device, key: str):
+        d = torch.device(device)
+        if d.index is None:
+            d = torch.device(d.type, torch.cuda.current_device())
+        return (str(d), torch.cuda.current_stream(d).cuda_stream, key)
+
     def peek(self, device, key: str = "default") -> torch.Tensor | None:
-        device = torch.device(device)
-        return self._bufs.get((str(device), torch.cuda.current_stream(device).cuda_stream, key))
+        return self._bufs.get(self._key(device, key))
 
     def get(self, device, nbytes: int, key: str = "default") -> torch.Tensor:
-        k = (str(device), torch.cuda.current_stream(device).cuda_stream, key)
+        k = self._key(device, key)
         buf = self._bufs.get(k)
         if buf is None or buf.numel() < nbytes:
             # 256-byte alignment comes from the caching allocator (512 B).
