@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define RMOE_ABI_VERSION 3
+#define RMOE_ABI_VERSION 4
 
 #define RMOE_OK 0
 #define RMOE_EINVAL (-1) /* inconsistent or unsupported shape / argument */
@@ -214,6 +214,26 @@ int rmoe_moe_block(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
                    const uint16_t* residual, uint16_t* out,
                    int32_t* indices_out, float* scores_out, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/* rmoe_moe_block without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference (its
+ * probes own every buffer).  The call allocates nothing: its scratch is a
+ * static device array of RMOE_NOALLOC_SCRATCH_BYTES held by each GPU the
+ * library runs on until the process ends; a call that needs more
+ * (rmoe_workspace_bytes(layer, tokens) > RMOE_NOALLOC_SCRATCH_BYTES, e.g.
+ * long prefills) is refused with RMOE_EWS before anything is launched.
+ * Every call on one GPU shares that array: calls that may overlap on one
+ * GPU (different streams, different host threads) race and must be
+ * serialised by the caller.  Arguments and outputs as rmoe_moe_block;
+ * status_out (device uint32, may be NULL) receives this call's status word
+ * (nonzero: a single-launch decode gave up a cross-workgroup wait and the
+ * outputs are not valid), which the call then clears. */
+#define RMOE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int rmoe_moe_block_noalloc(const rmoe_layer* layer, const uint16_t* x, int32_t tokens,
+                           const uint16_t* residual, uint16_t* out,
+                           int32_t* indices_out, float* scores_out, uint32_t* status_out,
+                           void* stream);
 
 /* Batch-1 decode of one token through a stack of MoE layers with a residual
  * add between them: x_{l+1} = bf16(x_l + block_l(x_l)), one launch for the

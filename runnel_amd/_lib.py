@@ -22,7 +22,7 @@ RMOE_EHIP = -5
 RMOE_ENULL = -6
 RMOE_ETIMEOUT = -7
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EXPORTED = (
     "rmoe_abi_version", "rmoe_last_error", "rmoe_status_string",
@@ -32,8 +32,11 @@ EXPORTED = (
     "rmoe_router_workspace_bytes", "rmoe_chain_table_bytes", "rmoe_chain_table_pack",
     "rmoe_moe_chain", "rmoe_workspace_status_offset", "rmoe_router_q",
     "rmoe_switch_combine", "rmoe_switch_combine_workspace_bytes", "rmoe_rms_norm",
-    "rmoe_set_cooperative_launch",
+    "rmoe_set_cooperative_launch", "rmoe_moe_block_noalloc",
 )
+
+# rmoe_moe_block_noalloc's static scratch per GPU (RMOE_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 
 class RmoeError(RuntimeError):
@@ -113,6 +116,7 @@ def load() -> ctypes.CDLL:
         lib.rmoe_switch_combine_workspace_bytes.argtypes = [QP, QP, I32, I32]
         lib.rmoe_gather_qmm.argtypes = [P, I32, P, P, I32, QP, P, P, P]
         lib.rmoe_moe_block.argtypes = [LP, P, I32, P, P, P, P, P, SZ, P]
+        lib.rmoe_moe_block_noalloc.argtypes = [LP, P, I32, P, P, P, P, P, P]
         lib.rmoe_quantize.argtypes = [P, I64, I32, I32, I32, P, P, P, P]
         lib.rmoe_dequantize.argtypes = [QP, I64, I64, P, P, P]
         lib.rmoe_stream_read.argtypes = [P, SZ, P, I32, P]

@@ -13,6 +13,9 @@
 #include "kernels.h"
 #include "rmoe.h"
 
+static_assert(RMOE_NOALLOC_SCRATCH_BYTES == rmoe::kStaticScratchBytes,
+              "the header states the static scratch size");
+
 namespace {
 
 thread_local std::string g_error;
@@ -632,13 +635,17 @@ int rmoe_router_q(const rmoe_qweight* router, int32_t top_k, int32_t norm_topk_p
   return ok();
 }
 
-int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
-                   const uint16_t* residual, uint16_t* out, int32_t* indices_out,
-                   float* scores_out, void* ws, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Argument checks of a block call (everything but the workspace).
+int check_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
+                const uint16_t* residual, const uint16_t* out) {
   int rc;
   if ((rc = check_layer(L))) return rc;
   if ((rc = check_tokens(tokens))) return rc;
-  if (tokens == 0) return ok();
+  if (tokens == 0) return RMOE_OK;
   if (!x || !out) return fail(RMOE_ENULL, "x and out are required");
   if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
   if (!aligned(out, 2) || (residual && !aligned(residual, 2)))
@@ -650,7 +657,14 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
     return fail(RMOE_EALIGN,
                 "out/residual must be 16-byte aligned for calls that route %d or more "
                 "(token, slot) rows", rmoe::kPrefillMinRows);
-  if ((rc = check_ws(ws, ws_bytes, lay.total))) return rc;
+  return RMOE_OK;
+}
+
+// The block's launches on a checked call and a workspace of lay.total bytes.
+int block_launch(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
+                 const uint16_t* residual, uint16_t* out, int32_t* indices_out,
+                 float* scores_out, void* ws, void* stream) {
+  const Layout lay = block_layout(L, tokens);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int bits = L->gate_up.bits;
   int grid = 0;
@@ -704,6 +718,48 @@ int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   if (e != hipSuccess) return hip_fail(e, "gate/up launch");
   e = rmoe::launch_down(a, bits, true, s);
   if (e != hipSuccess) return hip_fail(e, "down launch");
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int rmoe_moe_block(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
+                   const uint16_t* residual, uint16_t* out, int32_t* indices_out,
+                   float* scores_out, void* ws, size_t ws_bytes, void* stream) {
+  int rc;
+  if ((rc = check_block(L, x, tokens, residual, out))) return rc;
+  if (tokens == 0) return ok();
+  if ((rc = check_ws(ws, ws_bytes, block_layout(L, tokens).total))) return rc;
+  return block_launch(L, x, tokens, residual, out, indices_out, scores_out, ws, stream);
+}
+
+int rmoe_moe_block_noalloc(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
+                           const uint16_t* residual, uint16_t* out, int32_t* indices_out,
+                           float* scores_out, uint32_t* status_out, void* stream) {
+  int rc;
+  if ((rc = check_block(L, x, tokens, residual, out))) return rc;
+  if (status_out && !aligned(status_out, 4))
+    return fail(RMOE_EALIGN, "status_out must be 4-byte aligned");
+  if (tokens == 0) return ok();
+  const size_t need = block_layout(L, tokens).total;
+  if (need > rmoe::kStaticScratchBytes)
+    return fail(RMOE_EWS,
+                "this call needs %zu bytes of scratch, more than the %zu bytes of the "
+                "library's static scratch; use rmoe_moe_block with a workspace",
+                need, rmoe::kStaticScratchBytes);
+  void* ws = nullptr;
+  hipError_t e = rmoe::static_scratch(&ws);
+  if (e != hipSuccess) return hip_fail(e, "static scratch address");
+  if ((rc = block_launch(L, x, tokens, residual, out, indices_out, scores_out, ws, stream)))
+    return rc;
+  if (status_out) {
+    e = rmoe::launch_take_status(
+        reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + rmoe_workspace_status_offset()),
+        status_out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "status launch");
+  }
   return ok();
 }
 

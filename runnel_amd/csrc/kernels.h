@@ -156,6 +156,13 @@ struct PrefillArgs {
   uint16_t* out;           // [T, H]
 };
 
+// ---- the static scratch of rmoe_moe_block_noalloc (noalloc.hip).
+constexpr size_t kStaticScratchBytes = size_t(16) << 20;
+// Device address of this device's copy (looked up once per device).
+hipError_t static_scratch(void** out);
+// *out = *word, then *word = 0 (one tiny kernel on `s`).
+hipError_t launch_take_status(uint32_t* word, uint32_t* out, hipStream_t s);
+
 int prefill_tile_rows(int T, int K, int E);
 int prefill_max_mtiles(int T, int K, int E, int bm);
 int prefill_sort_slices(int T, int K);

@@ -530,3 +530,24 @@ def test_status_word_is_read_cleared_and_raised():
     assert native.workspace_status(ws) == 0
     native.check_status(ws)
     assert b"timed out" in lib.rmoe_status_string(_lib.RMOE_ETIMEOUT)
+
+
+def test_noalloc_block_refuses_calls_beyond_its_static_scratch():
+    """rmoe_moe_block_noalloc checks the call's scratch need against its
+    fixed static array before it touches the device."""
+    lib = _lib.load()
+    L = _layer(H=2048, I=512, E=256, K=8)
+    T = 1
+    while lib.rmoe_workspace_bytes(ctypes.byref(L), T) <= _lib.NOALLOC_SCRATCH_BYTES:
+        T *= 2
+    rc = lib.rmoe_moe_block_noalloc(ctypes.byref(L), FAKE, T, None, FAKE + (1 << 24), None,
+                                    None, None, None)
+    assert rc == _lib.RMOE_EWS
+    assert b"static scratch" in lib.rmoe_last_error()
+    # argument errors come first, and zero tokens is a no-op
+    assert lib.rmoe_moe_block_noalloc(ctypes.byref(L), FAKE, 1, None, FAKE, None, None, None,
+                                      None) == _lib.RMOE_EINVAL   # out aliases x
+    assert lib.rmoe_moe_block_noalloc(ctypes.byref(L), FAKE, 1, None, FAKE + 4096, None, None,
+                                      FAKE + 2, None) == _lib.RMOE_EALIGN
+    assert lib.rmoe_moe_block_noalloc(ctypes.byref(L), FAKE, 0, None, FAKE + 4096, None, None,
+                                      None, None) == _lib.RMOE_OK
