@@ -503,11 +503,13 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
             row * 4, 0, kXcdStoreAux);
     }
 
-    // ---- K: poll all logits (wave 0), rank them, publish in LDS.
+    // ---- K: poll all logits (wave 0), rank them, publish the selection in
+    // LDS.  The softmax and the scores are only needed by D: wave 0 computes
+    // them after the routed loads are out (below), off the critical path.
+    float lv[kPer];
+    float m_top = 0.0f;
+    uint32_t my = 0, wsg = 0;
     if (wave == kPollWave) {
-      // the shared gate's logit, computed here (its row is not handed over)
-      uint32_t wsg = 0;
-      if (sg_row) wsg = f32_to_bf16(wave_sum(gate_partial(sw, s_in, lane))) << 16;
       // lane l holds experts 4 l .. 4 l + 3 (one 16-byte load from the L2)
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           sc->logits[xcd], (short)0, E * 4, 0x00020000);
@@ -526,7 +528,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         __builtin_amdgcn_s_sleep(1);
       }
       uint32_t k[kPer];
-      float lv[kPer];
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
         const int e = 4 * lane + i;
@@ -556,38 +557,13 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
           }
         }
       }
-      const float m = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
-      float z = 0.0f;
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-        if (4 * lane + i < E) z += __expf(lv[i] - m);
-      z = wave_sum(z);
+      m_top = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
       // slot j is handled by lane j
-      uint32_t my = 0;
 #pragma unroll
       for (int j = 0; j < NU - 1; ++j)
         if (lane == j) my = sel[j];
-      const float pb =
-          lane < K ? round_bf16(__expf(bf16_to_f32(bf16_from_order_key(my >> 16)) - m) / z) : 0.0f;
-      float total = 0.0f;  // slot order, as the oracle sums
-#pragma unroll
-      for (int j = 0; j < NU - 1; ++j)
-        if (j < K) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
-      if (lane < K) {
-        const int e = (int)(0xFFFFu - (my & 0xFFFFu));
-        // bf16 denominator, as mlx-lm's scores.sum(-1) of bf16 scores
-        const float score = p.norm ? round_bf16(pb / round_bf16(total)) : pb;
-        s_idx[lane] = e;
-        s_coef[lane] = score;
-        if (wg == 0 && last && p.idx_out) {
-          p.idx_out[lane] = e;
-          p.scores_out[lane] = score;
-        }
-      }
-      if (lane == 0 && p.has_shared) {
-        s_idx[K] = 0;
-        s_coef[K] = sg_row ? round_bf16(sigmoid(bf16_to_f32(wsg >> 16))) : 1.0f;
-      }
+      if (lane < K) s_idx[lane] = (int)(0xFFFFu - (my & 0xFFFFu));
+      if (lane == 0 && p.has_shared) s_idx[K] = 0;
     }
     __syncthreads();
 
@@ -663,6 +639,37 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     for (int u = 0; u < NU - 1; ++u)
       if (u < K && h < H) load_down_words<BITS>(dr[u], L.dn, (size_t)s_idx[u] * H + h, lane);
     issue_fence();
+
+    // ---- scores of the selection (wave 0, which does not poll act; read by D):
+    // softmax in fp32 over every expert, probabilities rounded to bf16,
+    // renormalised by the bf16 sum in slot order (mlx-lm's scores.sum(-1) of
+    // bf16 scores), quotient bf16; the shared gate bf16(sigmoid(logit)).
+    if (wave == kPollWave) {
+      // the shared gate's logit (its row is not handed over)
+      if (sg_row) wsg = f32_to_bf16(wave_sum(gate_partial(sw, s_in, lane))) << 16;
+      float z = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        if (4 * lane + i < E) z += __expf(lv[i] - m_top);
+      z = wave_sum(z);
+      const float pb =
+          lane < K ? round_bf16(__expf(bf16_to_f32(bf16_from_order_key(my >> 16)) - m_top) / z)
+                   : 0.0f;
+      float total = 0.0f;  // slot order, as the oracle sums
+#pragma unroll
+      for (int j = 0; j < NU - 1; ++j)
+        if (j < K) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
+      if (lane < K) {
+        const float score = p.norm ? round_bf16(pb / round_bf16(total)) : pb;
+        s_coef[lane] = score;
+        if (wg == 0 && last && p.idx_out) {
+          p.idx_out[lane] = (int)(0xFFFFu - (my & 0xFFFFu));
+          p.scores_out[lane] = score;
+        }
+      }
+      if (lane == 0 && p.has_shared)
+        s_coef[K] = sg_row ? round_bf16(sigmoid(bf16_to_f32(wsg >> 16))) : 1.0f;
+    }
 
     // ---- down scales / biases of every unit, ready before act arrives.
     const int gd = lane >> 3;
