@@ -105,8 +105,11 @@ __device__ __forceinline__ bf16x8_t dequant_frag(const uint4 (&w)[LPC], int j, f
     d.w = pack_bf16x2(fmaf((float)((w1 >> 16) & 0xFFu), s, b), fmaf((float)(w1 >> 24), s, b));
   } else {
     const uint32_t wj = word_of(w[j >> 2], j & 3);
-    const uint32_t lo = wj & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
-    const uint32_t hi = (wj >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
+    uint32_t lo = wj & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
+    uint32_t hi = (wj >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
+    // opaque to the optimiser: otherwise each code becomes a bit-field
+    // extract of wj plus a conversion, instead of one byte conversion
+    asm volatile("" : "+v"(lo), "+v"(hi));
     d.x = pack_bf16x2(fmaf((float)(lo & 0xFFu), s, b), fmaf((float)(hi & 0xFFu), s, b));
     d.y = pack_bf16x2(fmaf((float)((lo >> 8) & 0xFFu), s, b),
                       fmaf((float)((hi >> 8) & 0xFFu), s, b));
@@ -389,8 +392,10 @@ struct Gemm {
       const int pi = tid + THREADS * j;
       const int r = pi / (C::KC / 8);
       const int c8 = pi - r * (C::KC / 8);
-      *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) =
-          live[j] ? ar[j] : make_uint4(0, 0, 0, 0);
+      // rows past the tile's end hold a copy of a live row (or zeros, for
+      // the short tiles that load live rows only): they only reach output
+      // rows the epilogue does not store, so no select is needed
+      *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) = ar[j];
     }
   }
   // Scales and biases stay raw bf16 bits until the chunk that uses them, so
