@@ -194,7 +194,14 @@ size_t rmoe_switch_combine_workspace_bytes(const rmoe_qweight* gate_up,
  * y[m] = x[lhs[m]] . deq(w[rhs[m]])^T for m < rows.  lhs_indices == NULL
  * means row m reads x[m]; rhs_indices == NULL means expert 0; a row whose
  * index is out of range is written as zeros.  x bf16 [x_rows, w->cols];
- * exactly one of y_bf16 / y_f32 ([rows, w->rows]) is non-NULL. */
+ * exactly one of y_bf16 / y_f32 ([rows, w->rows]) is non-NULL.  Each row
+ * is a group-affine dot over fp32 weights fl32(q*s + b), except a dense
+ * product (no index arrays) of 64 or more rows into a 16-byte aligned
+ * y_bf16 with w->rows a multiple of 256 and w->cols a multiple of 128
+ * (mx.quantized_matmul at prefill sizes, the reference's qmm_4d_tile,
+ * native/shaders/quantized_qmm.metal:68-151): that one runs on the matrix
+ * cores with every dequantised weight rounded to bf16 and fp32
+ * accumulation. */
 int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows,
                     const int32_t* lhs_indices, const int32_t* rhs_indices,
                     int32_t rows, const rmoe_qweight* w, uint16_t* y_bf16,

@@ -788,16 +788,26 @@ int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows, const int32_t* lhs,
   if (rows < 0 || x_rows < 0) return fail(RMOE_EINVAL, "rows must be >= 0");
   if ((y_bf16 == nullptr) == (y_f32 == nullptr))
     return fail(RMOE_EINVAL, "exactly one of y_bf16 / y_f32 must be given");
+  const bool dense = !lhs && !rhs && y_bf16 && aligned(y_bf16, 16) &&
+                     rmoe::dense_qmm_eligible(rows, w->rows, w->cols);
   const int vpc = values_per_chunk(w->bits);
   const int chunks = w->cols / vpc;
-  if (chunks < 64 && !pow2(chunks))
+  if (!dense && chunks < 64 && !pow2(chunks))
     return fail(RMOE_EINVAL, "cols %d unsupported at %d bits", w->cols, w->bits);
-  if (chunks > 256)
+  if (!dense && chunks > 256)
     return fail(RMOE_EINVAL, "cols %d too large (max %d at %d bits)", w->cols,
                 256 * vpc, w->bits);
   if (rows == 0) return ok();
   if (!x) return fail(RMOE_ENULL, "x is required");
   if (!aligned(x, 16)) return fail(RMOE_EALIGN, "x must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dense) {
+    // a dense product at prefill sizes: the grouped GEMM on the matrix cores
+    const hipError_t e =
+        rmoe::launch_dense_qmm(x, rows, qw(*w), w->rows, w->cols, w->bits, y_bf16, s);
+    if (e != hipSuccess) return hip_fail(e, "dense qmm launch");
+    return ok();
+  }
   rmoe::QmvArgs a{};
   a.M = rows;
   a.N = w->rows;
@@ -810,7 +820,7 @@ int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows, const int32_t* lhs,
   a.w = qw(*w);
   a.y_bf16 = y_bf16;
   a.y_f32 = y_f32;
-  const hipError_t e = rmoe::launch_qmv(a, w->bits, static_cast<hipStream_t>(stream));
+  const hipError_t e = rmoe::launch_qmv(a, w->bits, s);
   if (e != hipSuccess) return hip_fail(e, "qmv launch");
   return ok();
 }

@@ -140,6 +140,7 @@ constexpr int kPrefillMinRows = 64;      // (token, slot) rows that select it
 struct PrefillArgs {
   int T, H, I, E, K, has_shared;
   int bm;                  // rows per m-tile (set by launch_prefill)
+  int dense;               // 1: rows 0..T-1 of expert 0 in order (no sort; tiles from T)
   const uint16_t* x;       // [T, H]
   const int32_t* idx;      // [T, K] expert ids (out of range -> zero rows)
   QW gu, dn, sgu, sdn;
@@ -167,5 +168,12 @@ int prefill_tile_rows(int T, int K, int E);
 int prefill_max_mtiles(int T, int K, int E, int bm);
 int prefill_sort_slices(int T, int K);
 hipError_t launch_prefill(const PrefillArgs& a, int bits, bool combine, hipStream_t s);
+// y[m] = x[m] . deq(w)^T on the matrix cores for M >= kDenseQmmMinRows rows
+// (mx.quantized_matmul at prefill sizes): every dequantised weight rounded
+// to bf16, fp32 accumulation, bf16 out.  Shapes: K % 128 == 0, N % 256 == 0.
+constexpr int kDenseQmmMinRows = 64;
+bool dense_qmm_eligible(int M, int N, int K);
+hipError_t launch_dense_qmm(const uint16_t* x, int M, const QW& w, int N, int K, int bits,
+                            uint16_t* y, hipStream_t s);
 
 }  // namespace rmoe

@@ -37,6 +37,8 @@
 // lane's operands come from one 16-byte load: within a chunk of KC values of
 // one row, lane group g = l / 16 owns k = g KC / 4 + [0, KC / 4), and MFMA j
 // of the chunk takes k = g KC / 4 + 8 j + [0, 8) for both A and B.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -135,7 +137,7 @@ struct Tile {
 // share its A rows in that XCD's L2, and the m-tiles of one expert share
 // its weight columns there.
 __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& t) {
-  const int MT = p.tile_offs[p.E + 2];
+  const int MT = p.dense ? (p.T + p.bm - 1) / p.bm : p.tile_offs[p.E + 2];
   const int total = nt * MT;
   const int L = (total + 7) >> 3;
   const int xcd = blockIdx.x & 7;
@@ -145,6 +147,13 @@ __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& 
   if (item >= total) return false;
   const int m = item / nt;
   t.n = item - m * nt;
+  if (p.dense) {
+    // rows m bm .. of the one bank, in order
+    t.bucket = 0;
+    t.row0 = m * p.bm;
+    t.nrows = min(p.bm, p.T - t.row0);
+    return true;
+  }
   const int4 d = reinterpret_cast<const int4*>(p.tile_desc)[m];
   t.bucket = d.x;
   t.row0 = d.y;
@@ -646,9 +655,13 @@ __attribute__((amdgpu_waves_per_eu(Chunk<BITS, BM, MODE>::MIN_WAVES))) void pref
   if (tid < BM) {
     int v = 0;
     if (tid < tile.nrows) {
-      const int src = p.rows[tile.row0 + tid];
-      // gate/up: the token of the row; down: where its output goes
-      v = MODE == 0 ? (src < TK ? src / p.K : src - TK) : src;
+      if (MODE == 1 && p.dense) {
+        v = tile.row0 + tid;  // a dense product writes row m of y
+      } else {
+        const int src = p.rows[tile.row0 + tid];
+        // gate/up: the token of the row; down: where its output goes
+        v = MODE == 0 ? (src < TK ? src / p.K : src - TK) : src;
+      }
     }
     s_row[tid] = v;
   }
@@ -766,6 +779,49 @@ void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn),
                      dim3(Chunk<BITS, BM, 1>::THREADS), 0, s,
                      a, nt_dn);
+}
+
+bool dense_qmm_eligible(int M, int N, int K) {
+  return M >= kDenseQmmMinRows && K >= 128 && K % 128 == 0 && N >= 256 && N % 256 == 0;
+}
+
+// The down GEMM's plain epilogue over a dense A: A = x rows in order (as the
+// activations), the bank's expert 0 as the weights, y rows in place.
+hipError_t launch_dense_qmm(const uint16_t* x, int M, const QW& w, int N, int K, int bits,
+                            uint16_t* y, hipStream_t s) {
+  PrefillArgs a{};
+  a.T = M;
+  a.K = 1;
+  a.E = 1;
+  a.H = N;       // output columns
+  a.I = K;       // reduction
+  a.dense = 1;
+  a.act = const_cast<uint16_t*>(x);
+  a.dn = w;
+  a.y = y;
+  // short products: 32-row tiles give more workgroups
+  a.bm = M <= 256 ? 32 : kPrefillBM;
+  const int mt = (M + a.bm - 1) / a.bm;
+  auto go = [&](auto bits_c, auto bm_c) {
+    constexpr int B = decltype(bits_c)::value;
+    constexpr int BMc = decltype(bm_c)::value;
+    const int nt = N / Gemm<B, BMc, 1>::TN;
+    const int g = 8 * ((nt * mt + 7) / 8);
+    hipLaunchKernelGGL((prefill_gemm_kernel<B, BMc, 1>), dim3(g),
+                       dim3(Chunk<B, BMc, 1>::THREADS), 0, s, a, nt);
+  };
+  using I8 = std::integral_constant<int, 8>;
+  using I4 = std::integral_constant<int, 4>;
+  using B32 = std::integral_constant<int, 32>;
+  using B128 = std::integral_constant<int, kPrefillBM>;
+  if (bits == 8) {
+    if (a.bm == 32) go(I8{}, B32{});
+    else go(I8{}, B128{});
+  } else {
+    if (a.bm == 32) go(I4{}, B32{});
+    else go(I4{}, B128{});
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs& args, int bits, bool combine, hipStream_t s) {
