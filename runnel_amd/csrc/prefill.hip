@@ -94,7 +94,11 @@ __device__ __forceinline__ uint32_t word_of(const uint4 v, int c) {
 
 // The bf16 MFMA fragment j (8 consecutive k) of a lane's weight slice (LPC
 // 16-byte loads).
-template <int BITS, int LPC>
+// OPAQUE (4 bits): keep the nibble-split words opaque to the optimiser,
+// which otherwise turns each code into a bit-field extract plus a
+// conversion instead of one byte conversion; it holds both words live, so
+// only the 128-row tiles (registers to spare) use it.
+template <int BITS, int LPC, bool OPAQUE>
 __device__ __forceinline__ bf16x8_t dequant_frag(const uint4 (&w)[LPC], int j, float s,
                                                  float b) {
   u32x4 d;
@@ -109,9 +113,7 @@ __device__ __forceinline__ bf16x8_t dequant_frag(const uint4 (&w)[LPC], int j, f
     const uint32_t wj = word_of(w[j >> 2], j & 3);
     uint32_t lo = wj & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
     uint32_t hi = (wj >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
-    // opaque to the optimiser: otherwise each code becomes a bit-field
-    // extract of wj plus a conversion, instead of one byte conversion
-    asm volatile("" : "+v"(lo), "+v"(hi));
+    if constexpr (OPAQUE) asm volatile("" : "+v"(lo), "+v"(hi));
     d.x = pack_bf16x2(fmaf((float)(lo & 0xFFu), s, b), fmaf((float)(hi & 0xFFu), s, b));
     d.y = pack_bf16x2(fmaf((float)((lo >> 8) & 0xFFu), s, b),
                       fmaf((float)((hi >> 8) & 0xFFu), s, b));
@@ -448,7 +450,7 @@ struct Gemm {
     bf16x8_t a[MBA], bf[QPW];
     read_a(0, a);
 #pragma unroll
-    for (int qq = 0; qq < QPW; ++qq) bf[qq] = dequant_frag<BITS, C::LPC>(w[qq], 0, s[qq], b[qq]);
+    for (int qq = 0; qq < QPW; ++qq) bf[qq] = dequant_frag<BITS, C::LPC, (BM >= 64)>(w[qq], 0, s[qq], b[qq]);
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
       bf16x8_t na[MBA], nbf[QPW];
@@ -456,7 +458,7 @@ struct Gemm {
         read_a(j + 1, na);
 #pragma unroll
         for (int qq = 0; qq < QPW; ++qq)
-          nbf[qq] = dequant_frag<BITS, C::LPC>(w[qq], j + 1, s[qq], b[qq]);
+          nbf[qq] = dequant_frag<BITS, C::LPC, (BM >= 64)>(w[qq], j + 1, s[qq], b[qq]);
       }
 #pragma unroll
       for (int mb = 0; mb < MBA; ++mb)
