@@ -308,6 +308,59 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   }
 }
 
+// ------------------------------------------------------------- epilogue
+// The tile's bf16 outputs go through LDS (the A buffers, free once every wave
+// has finished its last chunk) so that each row leaves in 16-byte pieces:
+// act rows (SwiGLU) in sorted order, or y rows at their (token, slot) place.
+// Wave w holds tile columns w 16 QPW + [0, 16 QPW): for gate/up the first
+// half of its blocks are up rows and the second half the matching gate rows,
+// so a wave's 8 QPW activation columns are local to it.
+// Rows are staged in LDS parts of RPP rows each (so[r / RPP]).
+template <int MODE, int MB, int QPW, int TN, int THREADS, int RPP>
+__device__ __forceinline__ void store_tile(const PrefillArgs& p, const Tile& tile,
+                                           const int* s_row, uint16_t* const* so,
+                                           const f32x4_t (&acc)[MB][QPW], int mba) {
+  constexpr int OS = TN + 8;  // LDS row stride (bf16)
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int col_l = tid & 15;
+  const int kg = (tid & 63) >> 4;
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    if (mb >= mba) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = mb * 16 + kg * 4 + i;
+      if constexpr (MODE == 0) {
+#pragma unroll
+        for (int h = 0; h < QPW / 2; ++h) {
+          const int c = wave * (8 * QPW) + h * 16 + col_l;
+          const float up = round_bf16(acc[mb][h][i]);
+          const float gate = round_bf16(acc[mb][QPW / 2 + h][i]);
+          so[r / RPP][(r % RPP) * OS + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
+        }
+      } else {
+#pragma unroll
+        for (int qq = 0; qq < QPW; ++qq) {
+          const int c = wave * (16 * QPW) + qq * 16 + col_l;
+          so[r / RPP][(r % RPP) * OS + c] = (uint16_t)f32_to_bf16(acc[mb][qq][i]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int PR = TN / 8;  // 16-byte pieces per row
+  for (int pi = tid; pi < tile.nrows * PR; pi += THREADS) {
+    const int r = pi / PR;
+    const int c8 = pi - r * PR;
+    const uint4 v = *reinterpret_cast<const uint4*>(so[r / RPP] + (r % RPP) * OS + c8 * 8);
+    uint16_t* dst = MODE == 0 ? p.act + (size_t)(tile.row0 + r) * p.I
+                              : p.y + (size_t)s_row[r] * p.H;
+    *reinterpret_cast<uint4*>(dst + tile.n * TN + c8 * 8) = v;
+  }
+}
+
 // ------------------------------------------------------------ grouped GEMM
 // MODE 0: gate/up.  A = x rows of the tile's tokens (K = H); the wave's four
 //         B column blocks are up rows c, c + 16 and gate rows I + c, I + c +
@@ -331,12 +384,13 @@ struct Gemm {
   QW q;
   static constexpr int QPW = C::QPW;
   static constexpr int THREADS = C::THREADS;
+  static constexpr int MIN_WAVES = C::MIN_WAVES;
+  static constexpr int LDS = C::STAGES * BM * C::ROW;  // bf16
   size_t brow[QPW];
   const uint32_t* wptr[QPW];
 
-  __device__ Gemm(const PrefillArgs& p_, const Tile& t_, uint16_t (*sa)[BM * C::ROW],
-                  const int* srow)
-      : p(p_), tile(t_), s_a(sa), s_row(srow) {
+  __device__ Gemm(const PrefillArgs& p_, const Tile& t_, uint16_t* lds, const int* srow)
+      : p(p_), tile(t_), s_a(reinterpret_cast<uint16_t (*)[BM * C::ROW]>(lds)), s_row(srow) {
     tid = threadIdx.x;
     wave = tid >> 6;
     lane = tid & 63;
@@ -597,58 +651,272 @@ struct Gemm {
     if (ch < nch) step<MBA, 0>(ch, nch, asrc, live, ar, bw, bs, bb, acc);
   }
 
-  // The tile's bf16 outputs go through LDS (the A buffers, free once every
-  // wave has finished its last chunk) so that each row leaves in 16-byte
-  // pieces: act rows (SwiGLU) in sorted order, or y rows at their (token,
-  // slot) place.
   __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
-    constexpr int OS = TN + 8;  // LDS row stride (bf16)
-    static_assert(BM * OS <= C::STAGES * BM * C::ROW, "output tile fits in the A buffers");
-    uint16_t* so = &s_a[0][0];
-    __syncthreads();
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      if (mb >= mba) continue;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = mb * 16 + kg * 4 + i;
-        if constexpr (MODE == 0) {
-#pragma unroll
-          for (int h = 0; h < QPW / 2; ++h) {
-            const int c = wave * (8 * QPW) + h * 16 + col_l;
-            const float up = round_bf16(acc[mb][h][i]);
-            const float gate = round_bf16(acc[mb][QPW / 2 + h][i]);
-            so[r * OS + c] = (uint16_t)f32_to_bf16(silu(gate) * up);
-          }
-        } else {
-#pragma unroll
-          for (int qq = 0; qq < QPW; ++qq) {
-            const int c = wave * (16 * QPW) + qq * 16 + col_l;
-            so[r * OS + c] = (uint16_t)f32_to_bf16(acc[mb][qq][i]);
-          }
-        }
-      }
-    }
-    __syncthreads();
-    constexpr int PR = TN / 8;  // 16-byte pieces per row
-    for (int pi = tid; pi < tile.nrows * PR; pi += THREADS) {
-      const int r = pi / PR;
-      const int c8 = pi - r * PR;
-      const uint4 v = *reinterpret_cast<const uint4*>(so + r * OS + c8 * 8);
-      uint16_t* dst = MODE == 0 ? p.act + (size_t)(tile.row0 + r) * p.I
-                                : p.y + (size_t)s_row[r] * p.H;
-      *reinterpret_cast<uint4*>(dst + tile.n * TN + c8 * 8) = v;
-    }
+    static_assert(BM * (TN + 8) <= C::STAGES * BM * C::ROW, "output tile fits in the A buffers");
+    uint16_t* so[1] = {&s_a[0][0]};
+    store_tile<MODE, MB, QPW, TN, THREADS, BM>(p, tile, s_row, so, acc, mba);
   }
 };
 
+// ------------------------------------------------------- 128-row tiles
+// Four waves per workgroup, two workgroups per CU.  Each wave owns 64 weight
+// columns (four 16-column blocks) of the 128-row tile, so every A fragment
+// read from LDS feeds four MFMAs: half the LDS reads per MFMA of 32-column
+// waves, which at the full matrix-core rate needed all of the LDS bandwidth.
+//
+// A reaches LDS without passing through registers: global_load_lds_dwordx4
+// writes 16 bytes per lane at (wave-uniform base + 16 lane), and each lane
+// fetches the piece that belongs at its position.  Four A stages of 64 k
+// values (16 KB each) are loaded three stages ahead; each stage ends with a
+// wait for this wave's copy of the next stage and a bare barrier, after which
+// that stage has landed for every wave (a fenced __syncthreads would wait
+// for every load in flight, the weights and the later stages included).  The
+// wait is counted: every stage issues the same loads in the same order, the
+// stages past the end reloading the last one into a buffer nobody reads, so
+// after the copy of stage c + 1 exactly 2 ND + NBL loads have been issued at
+// the end of stage c (fewer only in the first stage, where waiting for the
+// extra ones costs nothing: they are the weights in use).  Sched barriers
+// keep the compiler from reordering the load groups.
+//
+// Weights (B) stream into registers one chunk ahead (KB values: 128 at 4
+// bits, 64 at 8; 16 bytes of each of the wave's 4 columns per lane).
+//
+// LDS stage layout: row r holds 8 slots of 16 bytes; slot sl of row r sits at
+// position 8 r + (sl ^ f(r)), f(r) = (r & 7) ^ ((r >> 3) & 1).  An operand
+// read takes one slot (two, for the two lane groups of a half wave) of rows
+// r0 .. r0 + 15: any 8, 16 or 32 of its lanes then fall on distinct 16-byte
+// bank groups, whether the LDS has 64 or 128 banks (the plain XOR with r / 2
+// left 32-lane passes two-way conflicted).  Slot sl = 2 kg + j
+// holds the 8 k values that lane group kg feeds to k-step j of the stage:
+// k = (KB / 4) kg + 8 (2 h + j) + [0, 8) of the weight chunk, h = the
+// stage's index within its chunk, the k of the lane's B fragment.
+template <int BITS, int MODE>
+struct Wide {
+  static constexpr int BM = 128, MB = BM / 16, QPW = 4, WAVES = 4, THREADS = 64 * WAVES;
+  static constexpr int MIN_WAVES = 2;
+  static constexpr int TN = WAVES * 16 * QPW / (MODE == 0 ? 2 : 1);
+  static constexpr int KB = BITS == 4 ? 128 : 64;  // weight values per chunk
+  static constexpr int SB = KB / 64;               // A stages per weight chunk
+  static constexpr int STAGE = BM * 64;            // bf16 per A stage
+  static constexpr int NBUF = 4;
+  // each buffer also holds a quarter of the output tile (32 rows) in the epilogue
+  static constexpr int BUF = STAGE > (BM / NBUF) * (TN + 8) ? STAGE : (BM / NBUF) * (TN + 8);
+  static constexpr int NBL = 3 * QPW;  // load instructions per weight chunk
+
+  struct Bw {
+    u32x4 w[QPW];
+    uint32_t s[QPW], b[QPW];
+  };
+
+  const PrefillArgs& p;
+  const Tile& tile;
+  uint16_t *l0, *l1, *l2, *l3;  // four distinct LDS arrays
+  const int* s_row;
+  int tid, wave, lane, kg, nst, nbc;
+  // Buffer resources based at the tile's expert (offsets stay 32-bit) and
+  // this lane's byte offsets in them, per column block.
+  __amdgpu_buffer_rsrc_t rw, rs, rb, ra;
+  uint32_t woff[QPW], soff[QPW];
+
+  __device__ Wide(const PrefillArgs& p_, const Tile& t_, uint16_t* l0_, uint16_t* l1_,
+                  uint16_t* l2_, uint16_t* l3_, const int* srow)
+      : p(p_), tile(t_), l0(l0_), l1(l1_), l2(l2_), l3(l3_), s_row(srow) {
+    tid = threadIdx.x;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+    kg = lane >> 4;
+    const int col_l = lane & 15;
+    const bool shared = tile.bucket == p.E;
+    const size_t e = shared ? 0 : (size_t)tile.bucket;
+    const int K = MODE == 0 ? p.H : p.I;
+    const int N = MODE == 0 ? 2 * p.I : p.H;  // weight rows per expert
+    nst = K / 64;
+    nbc = K / KB;
+    const QW q = MODE == 0 ? (shared ? p.sgu : p.gu) : (shared ? p.sdn : p.dn);
+    const size_t WPR = (size_t)K * BITS / 32;  // u32 per weight row
+    const size_t G = (size_t)K / 64;           // groups per weight row
+    rw = __builtin_amdgcn_make_buffer_rsrc((void*)(q.w + e * N * WPR), (short)0,
+                                           (int)(N * WPR * 4), 0x00020000);
+    rs = __builtin_amdgcn_make_buffer_rsrc((void*)(q.s + e * N * G), (short)0, (int)(N * G * 2),
+                                           0x00020000);
+    rb = __builtin_amdgcn_make_buffer_rsrc((void*)(q.b + e * N * G), (short)0, (int)(N * G * 2),
+                                           0x00020000);
+    if constexpr (MODE == 0)
+      ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, (int)((size_t)p.T * p.H * 2),
+                                             0x00020000);
+    else
+      ra = __builtin_amdgcn_make_buffer_rsrc((void*)(p.act + (size_t)tile.row0 * p.I), (short)0,
+                                             tile.nrows * p.I * 2, 0x00020000);
+#pragma unroll
+    for (int qq = 0; qq < QPW; ++qq) {
+      uint32_t row;  // weight row within the expert
+      if constexpr (MODE == 0) {
+        // blocks 0, 1: up rows of the wave's 32 pairs; 2, 3: their gate rows
+        row = tile.n * TN + wave * 32 + (qq & 1) * 16 + col_l + (qq >> 1) * p.I;
+      } else {
+        row = tile.n * TN + wave * 64 + qq * 16 + col_l;
+      }
+      woff[qq] = (row * (uint32_t)WPR + kg * 4) * 4;
+      soff[qq] = row * (uint32_t)G * 2 + (BITS == 4 ? (kg >> 1) * 2 : 0);
+    }
+  }
+
+  // Weight chunk b of the wave's columns (16 bytes per lane and column) with
+  // the scale and bias of the lane's group.
+  __device__ __forceinline__ void load_b(int b, Bw& r) const {
+    const int wb = b * 64;                // bytes into each row's words
+    const int gb = b * (KB / 64) * 2;     // bytes into each row's groups
+#pragma unroll
+    for (int qq = 0; qq < QPW; ++qq) r.w[qq] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[qq], wb, 0);
+#pragma unroll
+    for (int qq = 0; qq < QPW; ++qq) {
+      r.s[qq] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[qq], gb, 0);
+      r.b[qq] = __builtin_amdgcn_raw_buffer_load_b16(rb, soff[qq], gb, 0);
+    }
+  }
+
+  // DMA instruction i of a stage covers tile rows 32 i + 8 wave + [0, 8);
+  // lane l writes slot position l & 7 of row 32 i + 8 wave + l / 8.  Byte
+  // offsets of the lane's pieces in the A resource.
+  __device__ __forceinline__ void a_src(uint32_t (&src)[MB / 2]) const {
+    const int rl = 8 * wave + (lane >> 3);  // row within each 32-row group
+    const int sl = (lane & 7) ^ ((rl & 7) ^ ((rl >> 3) & 1));
+    const int koff = BITS == 4 ? (4 * (sl >> 1) + (sl & 1)) * 8 : sl * 8;
+#pragma unroll
+    for (int i = 0; i < MB / 2; ++i) {
+      const int r = 32 * i + rl;
+      if constexpr (MODE == 0)
+        src[i] = ((uint32_t)s_row[r] * p.H + koff) * 2;  // s_row is token 0 past the end
+      else
+        src[i] = ((uint32_t)min(r, tile.nrows - 1) * p.I + koff) * 2;
+    }
+  }
+
+  // First k value of stage c in a row (the pieces of a stage start there).
+  __device__ __forceinline__ static int stage_col(int c) {
+    return BITS == 4 ? (c >> 1) * 128 + (c & 1) * 16 : c * 64;
+  }
+
+  template <int ND>
+  __device__ __forceinline__ void dma(uint16_t* buf, int c, const uint32_t (&src)[MB / 2]) const {
+    const int col = stage_col(c) * 2;
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (__attribute__((address_space(3))) void*)(buf + (i * 256 + wave * 64) * 8), 16,
+          src[i], col, 0, 0);
+  }
+
+  static constexpr int vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+  template <int BUF, int MBA>
+  __device__ __forceinline__ void stage(uint16_t* b0, uint16_t* b1, uint16_t* b2, uint16_t* b3,
+                                        int c, const uint32_t (&src)[MB / 2],
+                                        const int (&rd)[2], Bw& cur, Bw& nxt,
+                                        f32x4_t (&acc)[MB][QPW]) const {
+    constexpr int ND = MBA / 2;
+    constexpr int H = BUF % SB;
+    uint16_t* const bufs[NBUF] = {b0, b1, b2, b3};
+    __builtin_amdgcn_sched_barrier(0);
+    dma<ND>(bufs[(BUF + 3) % NBUF], min(c + 3, nst - 1), src);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (H == 0) {
+      load_b(min(c / SB + 1, nbc - 1), nxt);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint16_t* cb = bufs[BUF];
+    float sc[QPW], bi[QPW];
+#pragma unroll
+    for (int qq = 0; qq < QPW; ++qq) {
+      sc[qq] = bf16_to_f32(cur.s[qq]);
+      bi[qq] = bf16_to_f32(cur.b[qq]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16x8_t bf[QPW];
+#pragma unroll
+      for (int qq = 0; qq < QPW; ++qq)
+        bf[qq] = dequant_frag<BITS, 1, true>(
+            *reinterpret_cast<const uint4(*)[1]>(&cur.w[qq]), 2 * H + j, sc[qq], bi[qq]);
+#pragma unroll
+      for (int mb = 0; mb < MBA; ++mb) {
+        const bf16x8_t a =
+            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4*>(cb + mb * 1024 + rd[j]));
+#pragma unroll
+        for (int qq = 0; qq < QPW; ++qq) acc[mb][qq] = mfma(a, bf[qq], acc[mb][qq]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (H == SB - 1) cur = nxt;
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt(2 * ND + NBL));
+    __builtin_amdgcn_s_barrier();
+  }
+
+  template <int MBA>
+  __device__ __forceinline__ void pipeline(uint16_t* __restrict__ b0, uint16_t* __restrict__ b1,
+                                           uint16_t* __restrict__ b2, uint16_t* __restrict__ b3,
+                                           f32x4_t (&acc)[MB][QPW]) const {
+    constexpr int ND = MBA / 2;
+    uint32_t src[MB / 2];
+    a_src(src);
+    int rd[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      rd[j] = ((lane & 15) * 8 + ((2 * kg + j) ^ ((lane & 7) ^ ((lane >> 3) & 1)))) * 8;
+    Bw cur, nxt;
+    __builtin_amdgcn_sched_barrier(0);
+    dma<ND>(b0, 0, src);
+    __builtin_amdgcn_sched_barrier(0);
+    dma<ND>(b1, min(1, nst - 1), src);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(0, cur);
+    __builtin_amdgcn_sched_barrier(0);
+    dma<ND>(b2, min(2, nst - 1), src);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt(2 * ND + NBL));
+    __builtin_amdgcn_s_barrier();
+    int c = 0;
+    for (; c + 4 <= nst; c += 4) {
+      stage<0, MBA>(b0, b1, b2, b3, c, src, rd, cur, nxt, acc);
+      stage<1, MBA>(b0, b1, b2, b3, c + 1, src, rd, cur, nxt, acc);
+      stage<2, MBA>(b0, b1, b2, b3, c + 2, src, rd, cur, nxt, acc);
+      stage<3, MBA>(b0, b1, b2, b3, c + 3, src, rd, cur, nxt, acc);
+    }
+    if (c < nst) {  // K a multiple of 128: two stages left
+      stage<0, MBA>(b0, b1, b2, b3, c, src, rd, cur, nxt, acc);
+      stage<1, MBA>(b0, b1, b2, b3, c + 1, src, rd, cur, nxt, acc);
+    }
+  }
+
+  template <int MBA>
+  __device__ void run(f32x4_t (&acc)[MB][QPW]) const {
+    pipeline<MBA>(l0, l1, l2, l3, acc);
+  }
+
+  __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
+    uint16_t* so[NBUF] = {l0, l1, l2, l3};
+    store_tile<MODE, MB, QPW, TN, THREADS, BM / NBUF>(p, tile, s_row, so, acc, mba);
+  }
+};
+
+// The engine of a tile size: 128-row tiles on Wide, 32-row tiles on Gemm.
 template <int BITS, int BM, int MODE>
-__global__ __launch_bounds__((Chunk<BITS, BM, MODE>::THREADS))
-__attribute__((amdgpu_waves_per_eu(Chunk<BITS, BM, MODE>::MIN_WAVES))) void prefill_gemm_kernel(
-    const PrefillArgs p,
-                                                                     const int nt) {
-  using G = Gemm<BITS, BM, MODE>;
-  __shared__ __attribute__((aligned(16))) uint16_t s_a[G::C::STAGES][BM * G::C::ROW];
+struct EngineOf {
+  using type = Gemm<BITS, BM, MODE>;
+};
+template <int BITS, int MODE>
+struct EngineOf<BITS, 128, MODE> {
+  using type = Wide<BITS, MODE>;
+};
+template <int BITS, int BM, int MODE>
+using Engine = typename EngineOf<BITS, BM, MODE>::type;
+
+template <int BITS, int BM, int MODE>
+__global__ __launch_bounds__((Engine<BITS, BM, MODE>::THREADS))
+__attribute__((amdgpu_waves_per_eu(Engine<BITS, BM, MODE>::MIN_WAVES))) void prefill_gemm_kernel(
+    const PrefillArgs p, const int nt) {
+  using G = Engine<BITS, BM, MODE>;
   __shared__ int s_row[BM];
   Tile tile;
   if (!decode_tile(p, nt, tile)) return;
@@ -680,7 +948,21 @@ __attribute__((amdgpu_waves_per_eu(Chunk<BITS, BM, MODE>::MIN_WAVES))) void pref
     }
     return;
   }
-  const G g(p, tile, s_a, s_row);
+  // Wide: four distinct arrays, so that the compiler can tell the DMA into
+  // one stage from the reads of another (a single array makes it wait for
+  // every DMA in flight before each read)
+  constexpr bool kWide = BM == 128;
+  __shared__ __attribute__((aligned(16))) uint16_t s_l0[kWide ? Wide<BITS, MODE>::BUF : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_l1[kWide ? Wide<BITS, MODE>::BUF : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_l2[kWide ? Wide<BITS, MODE>::BUF : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_l3[kWide ? Wide<BITS, MODE>::BUF : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[kWide ? 1 : Gemm<BITS, BM, MODE>::LDS];
+  const G g = [&] {
+    if constexpr (kWide)
+      return G(p, tile, s_l0, s_l1, s_l2, s_l3, s_row);
+    else
+      return G(p, tile, s_lds, s_row);
+  }();
   f32x4_t acc[G::MB][G::QPW];
 #pragma unroll
   for (int mb = 0; mb < G::MB; ++mb)
@@ -771,16 +1053,14 @@ int prefill_max_mtiles(int T, int K, int E, int bm) {
 
 template <int BITS, int BM>
 void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
-  const int nt_gu = a.I / Gemm<BITS, BM, 0>::TN;
-  const int nt_dn = a.H / Gemm<BITS, BM, 1>::TN;
+  const int nt_gu = a.I / Engine<BITS, BM, 0>::TN;
+  const int nt_dn = a.H / Engine<BITS, BM, 1>::TN;
   const int g_gu = 8 * ((nt_gu * mt + 7) / 8);
   const int g_dn = 8 * ((nt_dn * mt + 7) / 8);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu),
-                     dim3(Chunk<BITS, BM, 0>::THREADS), 0, s,
-                     a, nt_gu);
+                     dim3(Engine<BITS, BM, 0>::THREADS), 0, s, a, nt_gu);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn),
-                     dim3(Chunk<BITS, BM, 1>::THREADS), 0, s,
-                     a, nt_dn);
+                     dim3(Engine<BITS, BM, 1>::THREADS), 0, s, a, nt_dn);
 }
 
 bool dense_qmm_eligible(int M, int N, int K) {
@@ -803,14 +1083,17 @@ hipError_t launch_dense_qmm(const uint16_t* x, int M, const QW& w, int N, int K,
   a.y = y;
   // short products: 32-row tiles give more workgroups
   a.bm = M <= 256 ? 32 : kPrefillBM;
+  if (a.bm == kPrefillBM && ((uint64_t)M * K * 2 > 0xFFFFFFFFull ||
+                             (uint64_t)N * K * bits / 8 > 0xFFFFFFFFull))
+    return hipErrorInvalidValue;
   const int mt = (M + a.bm - 1) / a.bm;
   auto go = [&](auto bits_c, auto bm_c) {
     constexpr int B = decltype(bits_c)::value;
     constexpr int BMc = decltype(bm_c)::value;
-    const int nt = N / Gemm<B, BMc, 1>::TN;
+    const int nt = N / Engine<B, BMc, 1>::TN;
     const int g = 8 * ((nt * mt + 7) / 8);
     hipLaunchKernelGGL((prefill_gemm_kernel<B, BMc, 1>), dim3(g),
-                       dim3(Chunk<B, BMc, 1>::THREADS), 0, s, a, nt);
+                       dim3(Engine<B, BMc, 1>::THREADS), 0, s, a, nt);
   };
   using I8 = std::integral_constant<int, 8>;
   using I4 = std::integral_constant<int, 4>;
@@ -826,9 +1109,20 @@ hipError_t launch_dense_qmm(const uint16_t* x, int M, const QW& w, int N, int K,
   return hipGetLastError();
 }
 
+// The 128-row tiles address x, the activations and one expert's weights
+// through buffer resources with 32-bit byte offsets.
+bool buffer_offsets_fit(const PrefillArgs& a, int bits) {
+  const uint64_t lim = 0xFFFFFFFFull;
+  const uint64_t x = (uint64_t)a.T * a.H * 2;
+  const uint64_t act = ((uint64_t)a.T * a.K + a.T) * a.I * 2;
+  const uint64_t w = (uint64_t)2 * a.I * a.H * bits / 8;  // one expert's gate/up or down
+  return x <= lim && act <= lim && w <= lim;
+}
+
 hipError_t launch_prefill(const PrefillArgs& args, int bits, bool combine, hipStream_t s) {
   PrefillArgs a = args;
   a.bm = prefill_tile_rows(a.T, a.K, a.E);
+  if (a.bm == kPrefillBM && !buffer_offsets_fit(a, bits)) return hipErrorInvalidValue;
   const int nw = prefill_sort_slices(a.T, a.K);
   hipLaunchKernelGGL(prefill_hist_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
   hipLaunchKernelGGL(prefill_place_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
