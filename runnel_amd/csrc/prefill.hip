@@ -38,6 +38,7 @@
 // one row, lane group g = l / 16 owns k = g KC / 4 + [0, KC / 4), and MFMA j
 // of the chunk takes k = g KC / 4 + 8 j + [0, 8) for both A and B.
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "kernels.h"
@@ -701,11 +702,18 @@ struct Wide {
   static constexpr int NBUF = 4;
   // each buffer also holds a quarter of the output tile (32 rows) in the epilogue
   static constexpr int BUF = STAGE > (BM / NBUF) * (TN + 8) ? STAGE : (BM / NBUF) * (TN + 8);
-  static constexpr int NBL = 3 * QPW;  // load instructions per weight chunk
+  static constexpr int NBL = QPW;  // load instructions per weight chunk
+  // Scales and biases come in blocks of 8 groups (16 bytes of a row), one
+  // block per PS stages: each lane loads the block of one of the wave's 64
+  // columns (lane l: column block l / 16, column l % 16) and ds_bpermute
+  // hands every lane the values of its column.  One block load per array
+  // and period replaces a 2-byte load per column block and chunk, each of
+  // which touched 16 rows: the memory pipeline, not the bytes, was the cost.
+  static constexpr int PS = 8 * 64 / KB * SB;  // stages per block (8 groups)
+  static constexpr int NSB = 2;                // block load instructions
 
   struct Bw {
     u32x4 w[QPW];
-    uint32_t s[QPW], b[QPW];
   };
 
   const PrefillArgs& p;
@@ -716,7 +724,8 @@ struct Wide {
   // Buffer resources based at the tile's expert (offsets stay 32-bit) and
   // this lane's byte offsets in them, per column block.
   __amdgpu_buffer_rsrc_t rw, rs, rb, ra;
-  uint32_t woff[QPW], soff[QPW];
+  uint32_t woff[QPW];
+  uint32_t soff;  // this lane's block row: column block lane / 16, column lane % 16
 
   __device__ Wide(const PrefillArgs& p_, const Tile& t_, uint16_t* l0_, uint16_t* l1_,
                   uint16_t* l2_, uint16_t* l3_, const int* srow)
@@ -757,21 +766,46 @@ struct Wide {
         row = tile.n * TN + wave * 64 + qq * 16 + col_l;
       }
       woff[qq] = (row * (uint32_t)WPR + kg * 4) * 4;
-      soff[qq] = row * (uint32_t)G * 2 + (BITS == 4 ? (kg >> 1) * 2 : 0);
+    }
+    {
+      const int qq = lane >> 4;
+      uint32_t row;
+      if constexpr (MODE == 0)
+        row = tile.n * TN + wave * 32 + (qq & 1) * 16 + col_l + (qq >> 1) * p.I;
+      else
+        row = tile.n * TN + wave * 64 + qq * 16 + col_l;
+      soff = row * (uint32_t)G * 2;
     }
   }
 
-  // Weight chunk b of the wave's columns (16 bytes per lane and column) with
-  // the scale and bias of the lane's group.
+  // Weight chunk b of the wave's columns (16 bytes per lane and column).
   __device__ __forceinline__ void load_b(int b, Bw& r) const {
-    const int wb = b * 64;                // bytes into each row's words
-    const int gb = b * (KB / 64) * 2;     // bytes into each row's groups
+    const int wb = b * 64;  // bytes into each row's words
 #pragma unroll
-    for (int qq = 0; qq < QPW; ++qq) r.w[qq] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[qq], wb, 0);
+    for (int qq = 0; qq < QPW; ++qq)
+      r.w[qq] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[qq], wb, 0);
+  }
+  // Scale and bias block k (groups 8 k .. 8 k + 7) of the lane's block row;
+  // groups past the row's end are never used.
+  __device__ __forceinline__ void load_blk(int k, u32x4& bs, u32x4& bb) const {
+    bs = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 16, 0);
+    bb = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 16, 0);
+  }
+  // The scale and bias (as floats) of chunk CIP of a block, for this lane's
+  // column and group: word (group / 2) from the lane that holds its column.
+  template <int CIP>
+  __device__ __forceinline__ void scales(const u32x4& bs, const u32x4& bb, float (&sc)[QPW],
+                                         float (&bi)[QPW]) const {
+    constexpr int G0 = CIP * KB / 64;  // first group of the chunk within the block
+    const int gi = BITS == 4 ? G0 + (kg >> 1) : G0;
+    const int sh = (gi & 1) * 16;
 #pragma unroll
     for (int qq = 0; qq < QPW; ++qq) {
-      r.s[qq] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[qq], gb, 0);
-      r.b[qq] = __builtin_amdgcn_raw_buffer_load_b16(rb, soff[qq], gb, 0);
+      const int from = 4 * (qq * 16 + (lane & 15));
+      const uint32_t vs = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)bs[G0 >> 1]);
+      const uint32_t vb = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)bb[G0 >> 1]);
+      sc[qq] = bf16_to_f32((vs >> sh) & 0xFFFFu);
+      bi[qq] = bf16_to_f32((vb >> sh) & 0xFFFFu);
     }
   }
 
@@ -809,13 +843,30 @@ struct Wide {
 
   static constexpr int vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-  template <int BUF, int MBA>
+  // Loads after the copy of A stage c + 1 by the end of stage c (POS = c %
+  // PS), counting only stages c - 1 and c: two A stages, the weights of the
+  // stages that start a chunk, the block loads of a period's first stage.
+  // In the first stages more have been issued: waiting for the extra ones
+  // costs nothing (they are in use).
+  template <int POS>
+  static constexpr int after_next(int nd) {
+    int n = 2 * nd;
+    for (int d = POS - 1; d <= POS; ++d) {
+      if ((d + PS) % SB == 0) n += NBL;
+      if ((d + PS) % PS == 0) n += NSB;
+    }
+    return n;
+  }
+
+  template <int POS, int MBA>
   __device__ __forceinline__ void stage(uint16_t* b0, uint16_t* b1, uint16_t* b2, uint16_t* b3,
                                         int c, const uint32_t (&src)[MB / 2],
-                                        const int (&rd)[2], Bw& cur, Bw& nxt,
-                                        f32x4_t (&acc)[MB][QPW]) const {
+                                        const int (&rd)[2], Bw& cur, Bw& nxt, u32x4& bs,
+                                        u32x4& bb, u32x4& nbs, u32x4& nbb, float (&sc)[QPW],
+                                        float (&bi)[QPW], f32x4_t (&acc)[MB][QPW]) const {
     constexpr int ND = MBA / 2;
-    constexpr int H = BUF % SB;
+    constexpr int BUF = POS % NBUF;
+    constexpr int H = POS % SB;
     uint16_t* const bufs[NBUF] = {b0, b1, b2, b3};
     __builtin_amdgcn_sched_barrier(0);
     dma<ND>(bufs[(BUF + 3) % NBUF], min(c + 3, nst - 1), src);
@@ -824,13 +875,12 @@ struct Wide {
       load_b(min(c / SB + 1, nbc - 1), nxt);
       __builtin_amdgcn_sched_barrier(0);
     }
-    const uint16_t* cb = bufs[BUF];
-    float sc[QPW], bi[QPW];
-#pragma unroll
-    for (int qq = 0; qq < QPW; ++qq) {
-      sc[qq] = bf16_to_f32(cur.s[qq]);
-      bi[qq] = bf16_to_f32(cur.b[qq]);
+    if constexpr (POS == 0) {
+      load_blk(c / PS + 1, nbs, nbb);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (H == 0) scales<POS / SB>(bs, bb, sc, bi);
+    const uint16_t* cb = bufs[BUF];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       bf16x8_t bf[QPW];
@@ -848,9 +898,35 @@ struct Wide {
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (H == SB - 1) cur = nxt;
+    if constexpr (POS == PS - 1) {
+      bs = nbs;
+      bb = nbb;
+    }
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(vmcnt(2 * ND + NBL));
+    __builtin_amdgcn_s_waitcnt(vmcnt(after_next<POS>(ND)));
     __builtin_amdgcn_s_barrier();
+  }
+
+  template <int MBA, int... P>
+  __device__ __forceinline__ void period(std::integer_sequence<int, P...>, uint16_t* b0,
+                                         uint16_t* b1, uint16_t* b2, uint16_t* b3, int c,
+                                         const uint32_t (&src)[MB / 2], const int (&rd)[2],
+                                         Bw& cur, Bw& nxt, u32x4& bs, u32x4& bb, u32x4& nbs,
+                                         u32x4& nbb, float (&sc)[QPW], float (&bi)[QPW],
+                                         f32x4_t (&acc)[MB][QPW]) const {
+    (stage<P, MBA>(b0, b1, b2, b3, c + P, src, rd, cur, nxt, bs, bb, nbs, nbb, sc, bi, acc), ...);
+  }
+  template <int MBA, int... P>
+  __device__ __forceinline__ void tail(std::integer_sequence<int, P...>, uint16_t* b0,
+                                       uint16_t* b1, uint16_t* b2, uint16_t* b3, int c,
+                                       const uint32_t (&src)[MB / 2], const int (&rd)[2],
+                                       Bw& cur, Bw& nxt, u32x4& bs, u32x4& bb, u32x4& nbs,
+                                       u32x4& nbb, float (&sc)[QPW], float (&bi)[QPW],
+                                       f32x4_t (&acc)[MB][QPW]) const {
+    ((c + P < nst ? stage<P, MBA>(b0, b1, b2, b3, c + P, src, rd, cur, nxt, bs, bb, nbs, nbb,
+                                  sc, bi, acc)
+                  : void()),
+     ...);
   }
 
   template <int MBA>
@@ -865,6 +941,10 @@ struct Wide {
     for (int j = 0; j < 2; ++j)
       rd[j] = ((lane & 15) * 8 + ((2 * kg + j) ^ ((lane & 7) ^ ((lane >> 3) & 1)))) * 8;
     Bw cur, nxt;
+    u32x4 bs, bb, nbs, nbb;
+    float sc[QPW], bi[QPW];
+    __builtin_amdgcn_sched_barrier(0);
+    load_blk(0, bs, bb);
     __builtin_amdgcn_sched_barrier(0);
     dma<ND>(b0, 0, src);
     __builtin_amdgcn_sched_barrier(0);
@@ -877,16 +957,12 @@ struct Wide {
     __builtin_amdgcn_s_waitcnt(vmcnt(2 * ND + NBL));
     __builtin_amdgcn_s_barrier();
     int c = 0;
-    for (; c + 4 <= nst; c += 4) {
-      stage<0, MBA>(b0, b1, b2, b3, c, src, rd, cur, nxt, acc);
-      stage<1, MBA>(b0, b1, b2, b3, c + 1, src, rd, cur, nxt, acc);
-      stage<2, MBA>(b0, b1, b2, b3, c + 2, src, rd, cur, nxt, acc);
-      stage<3, MBA>(b0, b1, b2, b3, c + 3, src, rd, cur, nxt, acc);
-    }
-    if (c < nst) {  // K a multiple of 128: two stages left
-      stage<0, MBA>(b0, b1, b2, b3, c, src, rd, cur, nxt, acc);
-      stage<1, MBA>(b0, b1, b2, b3, c + 1, src, rd, cur, nxt, acc);
-    }
+    for (; c + PS <= nst; c += PS)
+      period<MBA>(std::make_integer_sequence<int, PS>{}, b0, b1, b2, b3, c, src, rd, cur, nxt,
+                  bs, bb, nbs, nbb, sc, bi, acc);
+    if (c < nst)  // K not a multiple of PS * 64: the last stages, each guarded
+      tail<MBA>(std::make_integer_sequence<int, PS - 1>{}, b0, b1, b2, b3, c, src, rd, cur, nxt,
+                bs, bb, nbs, nbb, sc, bi, acc);
   }
 
   template <int MBA>
