@@ -92,6 +92,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 __device__ __forceinline__ uint32_t word_of(const uint4 v, int c) {
   return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
 }
+// Word i & 3 of v without indexing the vector (a run-time index would put
+// it in scratch memory).
+__device__ __forceinline__ uint32_t word4(const u32x4& v, int i) {
+  i &= 3;
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
 
 // The bf16 MFMA fragment j (8 consecutive k) of a lane's weight slice (LPC
 // 16-byte loads).
@@ -389,6 +395,14 @@ struct Gemm {
   static constexpr int LDS = C::STAGES * BM * C::ROW;  // bf16
   size_t brow[QPW];
   const uint32_t* wptr[QPW];
+  // Scales and biases come in blocks of 8 groups (16 bytes of a row) through
+  // bounds-checked buffer resources: lane l loads the block of the wave's
+  // column (l / 16) % QPW, l % 16 and ds_bpermute hands every lane the
+  // values of its column (one load per array and CPB chunks instead of a
+  // 2-byte load per column block and chunk, each touching 16 rows).
+  static constexpr int CPB = 8 * 64 / C::KC;  // chunks per block
+  __amdgpu_buffer_rsrc_t rs, rb;
+  uint32_t soff;
 
   __device__ Gemm(const PrefillArgs& p_, const Tile& t_, uint16_t* lds, const int* srow)
       : p(p_), tile(t_), s_a(reinterpret_cast<uint16_t (*)[BM * C::ROW]>(lds)), s_row(srow) {
@@ -415,6 +429,17 @@ struct Gemm {
       }
       wptr[qq] = q.w + brow[qq] * WPR + kg * C::LANE_WORDS;
     }
+    const size_t G = (size_t)K / 64;
+    const size_t rows = (MODE == 0 ? 2 * (size_t)p.I : (size_t)p.H) * (shared ? 1 : (size_t)p.E);
+    rs = __builtin_amdgcn_make_buffer_rsrc((void*)q.s, (short)0, (int)(rows * G * 2), 0x00020000);
+    rb = __builtin_amdgcn_make_buffer_rsrc((void*)q.b, (short)0, (int)(rows * G * 2), 0x00020000);
+    // lanes 32-63 hold the same blocks one word (two groups) on, for chunks
+    // whose lane groups need two different words (KC = 256)
+    size_t br = brow[0];  // (selected, not indexed: an index would put the object in memory)
+#pragma unroll
+    for (int qq = 1; qq < QPW; ++qq)
+      if (((lane >> 4) % QPW) == qq) br = brow[qq];
+    soff = (uint32_t)(br * G * 2) + (C::KC > 128 && lane >= 32 ? 4 : 0);
   }
 
   // This thread's A pieces: row base pointers, fixed for the whole tile.
@@ -464,21 +489,45 @@ struct Gemm {
       *reinterpret_cast<uint4*>(&s_a[buf][r * C::ROW + c8 * 8]) = ar[j];
     }
   }
-  // Scales and biases stay raw bf16 bits until the chunk that uses them, so
-  // a prefetch is never waited for where it is issued.
-  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[QPW][C::LPC], uint32_t (&s)[QPW],
-                                         uint32_t (&b)[QPW]) const {
-    const int G = K / 64;
-    const int g = (ch * C::KC + kg * (C::KC / 4)) >> 6;  // this lane's group
-#pragma unroll
-    for (int qq = 0; qq < QPW; ++qq) {
-      s[qq] = q.s[brow[qq] * G + g];
-      b[qq] = q.b[brow[qq] * G + g];
-    }
+  __device__ __forceinline__ void load_b(int ch, uint4 (&w)[QPW][C::LPC]) const {
 #pragma unroll
     for (int qq = 0; qq < QPW; ++qq)
 #pragma unroll
       for (int l = 0; l < C::LPC; ++l) w[qq][l] = load16_stream(wptr[qq] + ch * C::WORDS + 4 * l);
+  }
+  // Block k (groups 8 k .. 8 k + 7) of the lane's block row; groups past the
+  // row's end are never used (and past the array read as zeros).
+  __device__ __forceinline__ void load_blk(int k, u32x4& bs, u32x4& bb) const {
+    bs = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 16, 0);
+    bb = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 16, 0);
+  }
+  // Scale and bias of chunk cip of a block (a constant once unrolled) for
+  // this lane's column and group: the lane's group is the chunk's first plus
+  // kg KC / 256 (KC / 4 values per lane group, 64 per group).
+  __device__ __forceinline__ void scales(int cip, const u32x4& bs, const u32x4& bb,
+                                         float (&sc)[QPW], float (&bi)[QPW]) const {
+    const int gi = cip * (C::KC / 64) + ((kg * C::KC) >> 8);
+    const int sh = (gi & 1) * 16;
+#pragma unroll
+    for (int qq = 0; qq < QPW; ++qq) {
+      const int from = 4 * (qq * 16 + col_l);
+      uint32_t vs, vb;
+      if constexpr (C::KC <= 128) {
+        // both groups of the chunk in word cip
+        const int w = cip * (C::KC / 128);
+        vs = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)word4(bs, w));
+        vb = (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)word4(bb, w));
+      } else {
+        // four groups in words 2 cip, 2 cip + 1: lane groups 2, 3 read word
+        // 2 cip of the shifted copy, which is word 2 cip + 1
+        const int w = 2 * cip;
+        const int from2 = from + (kg >> 1) * 128;
+        vs = (uint32_t)__builtin_amdgcn_ds_bpermute(from2, (int)word4(bs, w));
+        vb = (uint32_t)__builtin_amdgcn_ds_bpermute(from2, (int)word4(bb, w));
+      }
+      sc[qq] = bf16_to_f32((vs >> sh) & 0xFFFFu);
+      bi[qq] = bf16_to_f32((vb >> sh) & 0xFFFFu);
+    }
   }
 
   // One chunk of KC: NJ MFMA steps over the first MBA row blocks.  The LDS
@@ -487,15 +536,9 @@ struct Gemm {
   // SIMD work at the same time.
   template <int MBA>
   __device__ __forceinline__ void chunk(int buf, const uint4 (&w)[QPW][C::LPC],
-                                        const uint32_t (&sraw)[QPW], const uint32_t (&braw)[QPW],
+                                        const float (&s)[QPW], const float (&b)[QPW],
                                         f32x4_t (&acc)[MB][QPW]) const {
     const uint16_t* sa = &s_a[buf][col_l * C::ROW + kg * (C::KC / 4)];
-    float s[QPW], b[QPW];
-#pragma unroll
-    for (int qq = 0; qq < QPW; ++qq) {
-      s[qq] = bf16_to_f32(sraw[qq]);
-      b[qq] = bf16_to_f32(braw[qq]);
-    }
     auto read_a = [&](int j, bf16x8_t (&a)[MBA]) {
 #pragma unroll
       for (int mb = 0; mb < MBA; ++mb)
@@ -537,25 +580,6 @@ struct Gemm {
     }
   }
 
-  // Chunks are prefetched two ahead: weights into two register sets (B of
-  // chunk c + 2 is issued as soon as chunk c has consumed its set), A into
-  // two register sets that feed the LDS double buffer one chunk ahead.  A
-  // of chunk c + 2 is issued before chunk c's MFMAs and B after them, so
-  // the wait for A of chunk c + 1 leaves both in flight.  Prefetches past
-  // the last chunk reload the last chunk, so no branch splits the loop.
-  template <int MBA, int S>
-  __device__ __forceinline__ void step(int c, int nch, const uint16_t* const (&asrc)[C::PPT],
-                                       const bool (&live)[C::PPT], uint4 (&ar)[2][C::PPT],
-                                       uint4 (&bw)[2][QPW][C::LPC], uint32_t (&bs)[2][QPW],
-                                       uint32_t (&bb)[2][QPW], f32x4_t (&acc)[MB][QPW]) const {
-    load_a(min(c + 2, nch - 1), asrc, ar[S ^ 1]);
-    __builtin_amdgcn_sched_barrier(0);
-    chunk<MBA>(c & 1, bw[S], bs[S], bb[S], acc);
-    load_b(min(c + 2, nch - 1), bw[S], bs[S], bb[S]);
-    store_a((c & 1) ^ 1, ar[S], live);
-    __syncthreads();
-  }
-
   // 32-row tiles (registers for four waves per SIMD): everything one chunk
   // ahead.
   template <int MBA>
@@ -566,46 +590,58 @@ struct Gemm {
     a_rows(asrc, live);
     uint4 ar[C::PPT];
     uint4 bw[QPW][C::LPC];
-    uint32_t bs[QPW], bb[QPW];
-    load_b(0, bw, bs, bb);
+    u32x4 bs, bb;
+    float sc[QPW], bi[QPW];
+    load_blk(0, bs, bb);
+    load_b(0, bw);
     load_a_live(0, asrc, live, ar);
     store_a(0, ar, live);
     __syncthreads();
-    for (int ch = 0; ch < nch; ++ch) {
-      const int nx = min(ch + 1, nch - 1);
-      uint4 nw[QPW][C::LPC];
-      uint32_t ns[QPW], nb[QPW];
-      load_b(nx, nw, ns, nb);
-      load_a_live(nx, asrc, live, ar);
-      chunk<MBA>(ch & 1, bw, bs, bb, acc);
-      store_a((ch & 1) ^ 1, ar, live);
-      __syncthreads();
+    for (int ch0 = 0; ch0 < nch; ch0 += CPB) {
 #pragma unroll
-      for (int qq = 0; qq < QPW; ++qq) {
+      for (int i = 0; i < CPB; ++i) {
+        const int ch = ch0 + i;
+        if (ch < nch) {
+          const int nx = min(ch + 1, nch - 1);
+          uint4 nw[QPW][C::LPC];
+          load_b(nx, nw);
+          load_a_live(nx, asrc, live, ar);
+          scales(i, bs, bb, sc, bi);
+          // the next block into the same registers, in flight during the
+          // block's last chunk (the chunk's closing barrier waits for it)
+          if (i == CPB - 1) load_blk(ch0 / CPB + 1, bs, bb);
+          chunk<MBA>(ch & 1, bw, sc, bi, acc);
+          store_a((ch & 1) ^ 1, ar, live);
+          __syncthreads();
 #pragma unroll
-        for (int l = 0; l < C::LPC; ++l) bw[qq][l] = nw[qq][l];
-        bs[qq] = ns[qq];
-        bb[qq] = nb[qq];
+          for (int qq = 0; qq < QPW; ++qq)
+#pragma unroll
+            for (int l = 0; l < C::LPC; ++l) bw[qq][l] = nw[qq][l];
+        }
       }
     }
   }
 
   // Down with K <= STAGES chunks: every A chunk is loaded and stored once up
-  // front (one barrier for the whole tile); weights stream two chunks ahead.
+  // front (one barrier for the whole tile); weights stream two chunks ahead;
+  // the scales and biases of at most 8 groups are one block.
   template <int MBA>
   __device__ void run_full(f32x4_t (&acc)[MB][QPW]) const {
+    static_assert(C::STAGES <= CPB, "one scale / bias block covers the tile's K");
     const int nch = K / C::KC;
     const uint16_t* asrc[C::PPT];
     bool live[C::PPT];
     a_rows(asrc, live);
     uint4 bw[2][QPW][C::LPC];
-    uint32_t bs[2][QPW], bb[2][QPW];
+    u32x4 bs, bb;
+    float sc[QPW], bi[QPW];
     uint4 ar[C::STAGES][C::PPT];
 #pragma unroll
     for (int c = 0; c < C::STAGES; ++c)
-      if (BM == 32 ? (c < nch) : true) load_a_live(min(c, nch - 1), asrc, live, ar[c]);
-    load_b(0, bw[0], bs[0], bb[0]);
-    load_b(min(1, nch - 1), bw[1], bs[1], bb[1]);
+      if (c < nch) load_a_live(min(c, nch - 1), asrc, live, ar[c]);
+    load_blk(0, bs, bb);
+    load_b(0, bw[0]);
+    load_b(min(1, nch - 1), bw[1]);
 #pragma unroll
     for (int c = 0; c < C::STAGES; ++c)
       if (c < nch) store_a(c, ar[c], live);
@@ -614,42 +650,22 @@ struct Gemm {
     for (int c = 0; c < C::STAGES; ++c) {
       if (c >= nch) break;
       const int S = c & 1;
-      chunk<MBA>(c, bw[S], bs[S], bb[S], acc);
-      load_b(min(c + 2, nch - 1), bw[S], bs[S], bb[S]);
+      scales(c, bs, bb, sc, bi);
+      chunk<MBA>(c, bw[S], sc, bi, acc);
+      load_b(min(c + 2, nch - 1), bw[S]);
     }
   }
 
   template <int MBA>
   __device__ void run(f32x4_t (&acc)[MB][QPW]) const {
+    static_assert(BM == 32, "128-row tiles run on the Wide engine");
     if constexpr (MODE == 1) {
       if (K <= C::STAGES * C::KC) {
         run_full<MBA>(acc);
         return;
       }
     }
-    if constexpr (BM == 32) {
-      run1<MBA>(acc);
-      return;
-    }
-    const int nch = K / C::KC;
-    const uint16_t* asrc[C::PPT];
-    bool live[C::PPT];
-    a_rows(asrc, live);
-    uint4 a0[C::PPT], ar[2][C::PPT];
-    uint4 bw[2][QPW][C::LPC];
-    uint32_t bs[2][QPW], bb[2][QPW];
-    load_a(0, asrc, a0);
-    load_b(0, bw[0], bs[0], bb[0]);
-    load_a(min(1, nch - 1), asrc, ar[0]);
-    load_b(min(1, nch - 1), bw[1], bs[1], bb[1]);
-    store_a(0, a0, live);
-    __syncthreads();
-    int ch = 0;
-    for (; ch + 1 < nch; ch += 2) {
-      step<MBA, 0>(ch, nch, asrc, live, ar, bw, bs, bb, acc);
-      step<MBA, 1>(ch + 1, nch, asrc, live, ar, bw, bs, bb, acc);
-    }
-    if (ch < nch) step<MBA, 0>(ch, nch, asrc, live, ar, bw, bs, bb, acc);
+    run1<MBA>(acc);
   }
 
   __device__ void epilogue(const f32x4_t (&acc)[MB][QPW], int mba) const {
