@@ -62,39 +62,51 @@ __device__ __forceinline__ void finish_route(const DecodeArgs& p, int t, const f
   }
 }
 
-// One lane's partial of a bf16 gate row (the router contract): chunks
-// lane + 64 i of 8 values, element by element.  All loads of a batch are
-// issued before the first multiply (one memory round trip per batch).
-__device__ __forceinline__ float bf16_gate_partial(const uint16_t* wr, const uint16_t* xt, int H,
-                                                   int lane) {
-  float acc = 0.0f;
+// One lane's partials of a bf16 gate row (the router contract) for TB
+// tokens (rows x, x + xs, ...; tokens >= nt are skipped): chunks lane + 64 i
+// of 8 values, element by element.  The row is loaded once for all tokens;
+// all loads of a batch are issued before the first multiply (one memory
+// round trip per batch).
+template <int TB>
+__device__ __forceinline__ void bf16_gate_partials(const uint16_t* wr, const uint16_t* x,
+                                                   size_t xs, int nt, int H, int lane,
+                                                   float (&acc)[TB]) {
+#pragma unroll
+  for (int k = 0; k < TB; ++k) acc[k] = 0.0f;
   const int chunks = H >> 3;
   for (int c0 = lane; c0 < chunks; c0 += 64 * kRouterBatch) {
-    uint4 xv[kRouterBatch], wv[kRouterBatch];
+    uint4 wv[kRouterBatch], xv[TB][kRouterBatch];
 #pragma unroll
     for (int i = 0; i < kRouterBatch; ++i) {
       const int c = c0 + 64 * i;
-      xv[i] = wv[i] = make_uint4(0, 0, 0, 0);
-      if (c < chunks) {
-        xv[i] = load16(xt + c * 8);
-        wv[i] = load16_stream(wr + c * 8);
+      wv[i] = make_uint4(0, 0, 0, 0);
+      if (c < chunks) wv[i] = load16_stream(wr + c * 8);
+#pragma unroll
+      for (int k = 0; k < TB; ++k) {
+        xv[k][i] = make_uint4(0, 0, 0, 0);
+        if (c < chunks && k < nt) xv[k][i] = load16(x + k * xs + c * 8);
       }
     }
 #pragma unroll
-    for (int i = 0; i < kRouterBatch; ++i) {
-      if (c0 + 64 * i < chunks) {
-        acc = fmaf(bf16_lo(xv[i].x), bf16_lo(wv[i].x), acc);
-        acc = fmaf(bf16_hi(xv[i].x), bf16_hi(wv[i].x), acc);
-        acc = fmaf(bf16_lo(xv[i].y), bf16_lo(wv[i].y), acc);
-        acc = fmaf(bf16_hi(xv[i].y), bf16_hi(wv[i].y), acc);
-        acc = fmaf(bf16_lo(xv[i].z), bf16_lo(wv[i].z), acc);
-        acc = fmaf(bf16_hi(xv[i].z), bf16_hi(wv[i].z), acc);
-        acc = fmaf(bf16_lo(xv[i].w), bf16_lo(wv[i].w), acc);
-        acc = fmaf(bf16_hi(xv[i].w), bf16_hi(wv[i].w), acc);
+    for (int k = 0; k < TB; ++k) {
+#pragma unroll
+      for (int i = 0; i < kRouterBatch; ++i) {
+        if (c0 + 64 * i < chunks) {
+          float a = acc[k];
+          const uint4 v = xv[k][i], w = wv[i];
+          a = fmaf(bf16_lo(v.x), bf16_lo(w.x), a);
+          a = fmaf(bf16_hi(v.x), bf16_hi(w.x), a);
+          a = fmaf(bf16_lo(v.y), bf16_lo(w.y), a);
+          a = fmaf(bf16_hi(v.y), bf16_hi(w.y), a);
+          a = fmaf(bf16_lo(v.z), bf16_lo(w.z), a);
+          a = fmaf(bf16_hi(v.z), bf16_hi(w.z), a);
+          a = fmaf(bf16_lo(v.w), bf16_lo(w.w), a);
+          a = fmaf(bf16_hi(v.w), bf16_hi(w.w), a);
+          acc[k] = a;
+        }
       }
     }
   }
-  return acc;
 }
 
 // 16 bf16 inputs (two 16-byte pieces) as floats.
@@ -107,76 +119,100 @@ __device__ __forceinline__ void unpack_x16(const uint4 a, const uint4 b, float (
   }
 }
 
-// One lane's partial of row `row` of an 8-bit MLX-affine gate bank (the
-// quantized router contract): chunks lane + 64 i of 16 codes.
-__device__ __forceinline__ float q8_gate_partial(const QW& bank, size_t row, const uint16_t* xt,
-                                                 int H, int lane) {
+// One lane's partials of row `row` of an 8-bit MLX-affine gate bank (the
+// quantized router contract) for TB tokens: chunks lane + 64 i of 16 codes.
+template <int TB>
+__device__ __forceinline__ void q8_gate_partials(const QW& bank, size_t row, const uint16_t* x,
+                                                 size_t xs, int nt, int H, int lane,
+                                                 float (&acc)[TB]) {
+#pragma unroll
+  for (int k = 0; k < TB; ++k) acc[k] = 0.0f;
   const int chunks = H >> 4;
   const uint32_t* wr = bank.w + row * (size_t)(H >> 2);
   const uint16_t* sr = bank.s + row * (size_t)(H >> 6);
   const uint16_t* br = bank.b + row * (size_t)(H >> 6);
-  float acc = 0.0f;
   for (int c0 = lane; c0 < chunks; c0 += 64 * kRouterBatch) {
-    uint4 wv[kRouterBatch], xa[kRouterBatch], xb[kRouterBatch];
+    uint4 wv[kRouterBatch], xa[TB][kRouterBatch], xb[TB][kRouterBatch];
     uint32_t sv[kRouterBatch], bv[kRouterBatch];
 #pragma unroll
     for (int i = 0; i < kRouterBatch; ++i) {
       const int c = c0 + 64 * i;
-      wv[i] = xa[i] = xb[i] = make_uint4(0, 0, 0, 0);
+      wv[i] = make_uint4(0, 0, 0, 0);
       sv[i] = bv[i] = 0;
       if (c < chunks) {
         wv[i] = load16_stream(wr + c * 4);
-        xa[i] = load16(xt + c * 16);
-        xb[i] = load16(xt + c * 16 + 8);
         sv[i] = sr[c >> 2];
         bv[i] = br[c >> 2];
       }
+#pragma unroll
+      for (int k = 0; k < TB; ++k) {
+        xa[k][i] = xb[k][i] = make_uint4(0, 0, 0, 0);
+        if (c < chunks && k < nt) {
+          xa[k][i] = load16(x + k * xs + c * 16);
+          xb[k][i] = load16(x + k * xs + c * 16 + 8);
+        }
+      }
     }
 #pragma unroll
-    for (int i = 0; i < kRouterBatch; ++i) {
-      if (c0 + 64 * i < chunks) {
-        float v[16];
-        unpack_x16(xa[i], xb[i], v);
-        acc = qgate_chunk(acc, wv[i], v, bf16_to_f32(sv[i]), bf16_to_f32(bv[i]));
+    for (int k = 0; k < TB; ++k) {
+#pragma unroll
+      for (int i = 0; i < kRouterBatch; ++i) {
+        if (c0 + 64 * i < chunks) {
+          float v[16];
+          unpack_x16(xa[k][i], xb[k][i], v);
+          acc[k] = qgate_chunk(acc[k], wv[i], v, bf16_to_f32(sv[i]), bf16_to_f32(bv[i]));
+        }
       }
     }
   }
-  return acc;
 }
 
-template <int P>
+// One wave per router row and group of TB tokens (grid.y): the row is
+// streamed once for the group.  The last workgroup of a group ranks its
+// tokens, one wave per token.
+template <int P, int TB>
 __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
-  const int t = blockIdx.y;
+  static_assert(TB >= 1 && TB <= 4, "one ranking wave per token");
+  const int g = blockIdx.y;
+  const int t0 = g * TB;
+  const int nt = p.T - t0 < TB ? p.T - t0 : TB;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int has_sg = p.has_sg;
   const int R = p.E + has_sg;
   const int row = blockIdx.x * 4 + wave;
-  const uint16_t* xt = p.x + (size_t)t * p.H;
-  float* lg = p.logits + (size_t)t * (p.E + 1);
+  const size_t ls = (size_t)(p.E + 1);
   if (row < R) {
-    float acc;
+    float acc[TB];
+    const uint16_t* xt = p.x + (size_t)t0 * p.H;
     if (p.rq8)
-      acc = q8_gate_partial(row < p.E ? p.rq : p.sgq, row < p.E ? (size_t)row : 0, xt, p.H,
-                            lane);
+      q8_gate_partials<TB>(row < p.E ? p.rq : p.sgq, row < p.E ? (size_t)row : 0, xt,
+                           (size_t)p.H, nt, p.H, lane, acc);
     else
-      acc = bf16_gate_partial(row < p.E ? p.router_w + (size_t)row * p.H : p.sgate_w, xt, p.H,
-                              lane);
-    acc = wave_sum(acc);
-    if (lane == 0) store_coherent(lg + row, acc);
+      bf16_gate_partials<TB>(row < p.E ? p.router_w + (size_t)row * p.H : p.sgate_w, xt,
+                             (size_t)p.H, nt, p.H, lane, acc);
+#pragma unroll
+    for (int k = 0; k < TB; ++k) {
+      if (k < nt) {
+        const float v = wave_sum(acc[k]);
+        if (lane == 0) store_coherent(p.logits + (t0 + k) * ls + row, v);
+      }
+    }
   }
 
-  // Last workgroup of this token ranks the logits.
+  // Last workgroup of this token group ranks the logits.
   __shared__ uint32_t s_last;
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = atomic_add_agent(&p.ctr[t], 1u);
+    const uint32_t prev = atomic_add_agent(&p.ctr[g], 1u);
     s_last = (prev == gridDim.x - 1) ? 1u : 0u;
   }
   __syncthreads();
-  if (s_last == 0u || wave != 0) return;
+  if (s_last == 0u || wave >= nt) return;
 
+  const int t = t0 + wave;
+  const float* lg = p.logits + t * ls;
   float lv[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
@@ -185,8 +221,8 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   }
   const float sg_logit = has_sg ? load_coherent(lg + p.E) : 0.0f;
   finish_route<P>(p, t, lv, sg_logit);
-  if (lane == 0)
-    __hip_atomic_store(&p.ctr[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave == 0 && lane == 0)
+    __hip_atomic_store(&p.ctr[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------ prefill router (MFMA)
@@ -709,6 +745,43 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
   const int H = p.H;
   const float* act_t = p.act + (size_t)t * U1 * I;
   const int CHR = I / VPC;  // chunks per row: power of two <= 64
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int RPL = 64 / CHR;
+  const int r = lane / CHR;
+  const int ch = lane - r * CHR;
+  const int h0 = (blk * 4 + wave) * RPL;
+  const int h = h0 + r;
+  const bool valid = h0 < H && h < H;
+  const int WPR = I / Packing<BITS>::kValuesPerWord;
+  const int G = I >> 6;
+  const int grp = (ch * VPC) >> 6;
+
+  // The weights of a batch of units depend on the routing only: they are
+  // issued before the activations are staged, so the two round trips
+  // overlap.
+  uint4 wv[kUnitBatch];
+  float sv[kUnitBatch], bv[kUnitBatch];
+  auto load_batch = [&](int u0) {
+#pragma unroll
+    for (int b = 0; b < kUnitBatch; ++b) {
+      const int u = u0 + b;
+      wv[b] = make_uint4(0, 0, 0, 0);
+      sv[b] = bv[b] = 0.0f;
+      const bool sh = u >= p.K;
+      const int e = (u < units && !sh) ? p.idx[t * p.K + u] : 0;
+      if (u < units && valid && (unsigned)e < (unsigned)p.E) {
+        const QW q = sh ? p.sdn : p.dn;
+        const size_t row = (size_t)e * H + h;
+        wv[b] = load16_stream(q.w + row * WPR + ch * 4);
+        sv[b] = bf16_to_f32(q.s[row * G + grp]);
+        bv[b] = bf16_to_f32(q.b[row * G + grp]);
+      }
+    }
+  };
+  load_batch(0);
+
   // Transposed staging: value v of chunk ch of unit u at u*I + v*CHR + ch,
   // so the lanes of a row (consecutive ch) read consecutive banks.
   {
@@ -739,47 +812,27 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
       }
     }
   }
-  __syncthreads();
-
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int RPL = 64 / CHR;
-  const int r = lane / CHR;
-  const int ch = lane - r * CHR;
-  const int h0 = (blk * 4 + wave) * RPL;
+  // the LDS stores of every wave are done; the weight loads stay in flight
+  // (a fenced __syncthreads would wait for them too)
+  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));
+  __builtin_amdgcn_s_barrier();
   if (h0 >= H) return;
-  const int h = h0 + r;
-  const bool valid = h < H;
-  const int WPR = I / Packing<BITS>::kValuesPerWord;
-  const int G = I >> 6;
-  const int grp = (ch * VPC) >> 6;
 
   float acc = 0.0f;
   for (int u0 = 0; u0 < units; u0 += kUnitBatch) {
-    uint4 wv[kUnitBatch];
-    float sv[kUnitBatch], bv[kUnitBatch];
-#pragma unroll
-    for (int b = 0; b < kUnitBatch; ++b) {
-      const int u = u0 + b;
-      wv[b] = make_uint4(0, 0, 0, 0);
-      sv[b] = bv[b] = 0.0f;
-      const bool sh = u >= p.K;
-      const int e = (u < units && !sh) ? p.idx[t * p.K + u] : 0;
-      if (u < units && valid && (unsigned)e < (unsigned)p.E) {
-        const QW q = sh ? p.sdn : p.dn;
-        const size_t row = (size_t)e * H + h;
-        wv[b] = load16_stream(q.w + row * WPR + ch * 4);
-        sv[b] = bf16_to_f32(q.s[row * G + grp]);
-        bv[b] = bf16_to_f32(q.b[row * G + grp]);
-      }
-    }
+    if (u0 > 0) load_batch(u0);  // top_k + shared above the batch size
 #pragma unroll
     for (int b = 0; b < kUnitBatch; ++b) {
       const int u = u0 + b;
       if (u >= units) continue;  // wave-uniform
       float a[VPC];
       float asum = 0.0f;
-      const float* src = s_act + u * I + ch;
+      // the unit's LDS offset is opaque to the optimiser: hoisting the
+      // read addresses of every unit out of the batch loop took 200+
+      // registers and left two waves per SIMD
+      int off = u * I + ch;
+      asm volatile("" : "+v"(off));
+      const float* src = s_act + off;
 #pragma unroll
       for (int v = 0; v < VPC; ++v) {
         a[v] = src[v * CHR];
@@ -928,13 +981,24 @@ hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, fl
   return hipSuccess;
 }
 
-hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
+template <int TB>
+static void router_tb(const DecodeArgs& a, hipStream_t s) {
   const int rows = a.E + a.has_sg;
-  dim3 grid((rows + 3) / 4, a.T);
+  dim3 grid((rows + 3) / 4, (a.T + TB - 1) / TB);
   if (a.E <= 256)
-    hipLaunchKernelGGL(router_kernel<4>, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((router_kernel<4, TB>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(router_kernel<kMaxExperts / 64>, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((router_kernel<kMaxExperts / 64, TB>), grid, dim3(256), 0, s, a);
+}
+
+hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
+  // tokens per group: each row is streamed once per group
+  if (a.T == 1)
+    router_tb<1>(a, s);
+  else if (a.T == 2)
+    router_tb<2>(a, s);
+  else
+    router_tb<4>(a, s);
   RMOE_CHECK_LAUNCH();
   return hipSuccess;
 }
