@@ -228,6 +228,61 @@ def run_decode_chain(args, torch):
     }
 
 
+def run_few_tokens(torch, stack, tokens, steps=20, warmup=3, seed=11):
+    """A few tokens through every layer of the stack, one block call per
+    layer (router, gate/up and down launches: the few-token kernels), each
+    layer's output plus residual feeding the next.  The passes over the
+    stack are replayed from a captured HIP graph; HIP events around them.
+    With 40 layers (34 GB) no layer's weights are still cached when it runs
+    again.  Bytes: every distinct expert the routing selects in each layer
+    (read once per call), the shared expert, the router, x, out and the
+    residual."""
+    import numpy as np
+    from runnel_amd import native, synthetic
+    H = 2048
+    handles = [lw.handle() for lw in stack]
+    bufs = [synthetic.make_x(seed, tokens, H), torch.empty((tokens, H), dtype=torch.bfloat16,
+                                                            device="cuda")]
+    ws = torch.zeros(handles[0].workspace_bytes(tokens), dtype=torch.uint8, device="cuda")
+    # the routing of one eager pass gives the distinct experts per layer
+    distinct = []
+    for l, h in enumerate(handles):
+        a, b = bufs[l & 1], bufs[(l + 1) & 1]
+        _, idx, _ = native.moe_block(h, a, residual=a, out=b, workspace=ws, return_routing=True)
+        distinct.append(len(np.unique(idx.cpu().numpy())))
+    per_expert = layer_bytes(H, 512, 256, 1, 8, shared=False, tokens=0) - 256 * H * 2
+    fixed = layer_bytes(H, 512, 256, 0, 8, shared=True, tokens=tokens, residual=True)
+    pass_bytes = sum(d * per_expert + fixed for d in distinct)
+
+    def one_pass():
+        for l, h in enumerate(handles):
+            a, b = bufs[l & 1], bufs[(l + 1) & 1]
+            native.moe_block(h, a, residual=a, out=b, workspace=ws)
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        one_pass()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_pass = e0.elapsed_time(e1) * 1000.0 / steps
+    us_call = us_pass / len(handles)
+    return {
+        "tokens": tokens, "layers": len(handles), "us_per_layer_call": round(us_call, 2),
+        "us_per_layer_token": round(us_call / tokens, 2),
+        "distinct_experts_per_layer": round(sum(distinct) / len(distinct), 2),
+        "hbm_gbps": round(pass_bytes / (us_pass * 1e-6) / 1e9, 1),
+        "launch": "graph (3 launches per layer call)",
+    }
+
+
 def prefill_flops(T, H, I, E, K, shared=True):
     rows = T * K + (T if shared else 0)
     return 2 * T * E * H + 2 * rows * (2 * I * H + H * I)
@@ -301,10 +356,11 @@ def main():
                     help="replay captured HIP graphs (default), launch eagerly every "
                          "step (cooperative launch), or eagerly with plain launches "
                          "(rmoe_set_cooperative_launch(0))")
-    ap.add_argument("--workload", choices=["decode40", "prefill512", "prefill8192"],
+    ap.add_argument("--workload", choices=["decode40", "prefill512", "prefill8192", "few"],
                     default="decode40",
-                    help="decode40: the bench line; the prefill workloads print "
-                         "their own line (exploration and profiling)")
+                    help="decode40: the bench line; the prefill workloads and few "
+                         "(2, 4 and 7 tokens through the 40-layer stack) print their "
+                         "own line (exploration and profiling)")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the prefill figures appended to the decode line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -322,6 +378,13 @@ def main():
     torch.cuda.synchronize()
     if args.calibrate_copy:
         return calibrate_copy(torch)
+    if args.workload == "few":
+        stack = build_stack(args.layers, 8)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": "few", "runs": [
+            run_few_tokens(torch, stack, T, args.steps, args.warmup) for T in (2, 4, 7)]}),
+            flush=True)
+        return 0
     if args.workload != "decode40":
         tokens, bits, skewed = (512, 8, False) if args.workload == "prefill512" else (8192, 4, True)
         r = run_prefill(torch, tokens, bits, skewed, args.steps, args.warmup)
@@ -376,6 +439,9 @@ def main():
             "frac_of_measured_read": round(achieved / read_gbps, 4),
         },
     }
+    if args.bits == 8 and args.gate_bits is None and not args.post_norm:
+        # 4 tokens per call through the same 40 layers (the few-token kernels)
+        out["few_token"] = run_few_tokens(torch, res["stack"], 4)
     if not args.no_prefill:
         # prefill figures of the same build (one layer per call, HIP events)
         out["prefill"] = {

@@ -217,6 +217,13 @@ __device__ __forceinline__ float qdot_chunk(const uint4 w, const float* v) {
 // contract: qa = sum q_i v_i and xs = sum v_i, each sequential from +0 (the
 // products are exact), then acc = fma(qa, s, acc), acc = fma(xs, b, acc)
 // with the chunk's group scale and bias.
+// Keep the compiler from moving loads or their uses across this point, so
+// that every load of a batch is issued before the first wait on any of them.
+__device__ __forceinline__ void issue_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ float qgate_chunk(float acc, const uint4 w, const float* v, float s,
                                              float b) {
   const float qa = qdot_chunk<8>(w, v);

@@ -17,6 +17,219 @@
 
 namespace rmoe {
 
+// --------------------------------------------------------------- few tokens
+// Calls of 2..8 tokens below the expert-sorted threshold (T K < 64) at the
+// single-launch shapes (hidden 2048, intermediate 512, 8-bit experts).  The
+// waves of each launch are resident at once (one round at up to 4 tokens):
+// a wave issues the loads of all its rows first and computes each row as
+// it lands, so the dequantisation runs under the stream instead of after
+// it.  The router launch also computes the shared expert's gate/up (which
+// does not depend on the routing), every pair for every token; the
+// activations go to the down kernel as bf16 (they are bf16-valued).
+namespace few {
+constexpr int H = kFusedH;
+constexpr int I = kFusedI;
+constexpr int G = H / 64;                 // groups per gate/up row (32)
+constexpr int NP = 8;                     // gate/up pairs per wave
+constexpr int kWavesPerUnit = I / NP;     // 64
+constexpr int kSharedPairs = 2;           // router launch: shared pairs per wave
+constexpr int kSharedBlocks = I / (4 * kSharedPairs);  // 64
+constexpr int kDownRows = 4;              // down rows per wave
+constexpr int kDownWavesPerToken = H / kDownRows;      // 512
+template <int BITS>
+struct Shape {
+  static constexpr int VPC = BITS == 8 ? 16 : 32;   // values per 16-byte chunk
+  static constexpr int CPL = H / VPC / 64;          // chunks per lane: 2 | 1
+  static constexpr int WPR = H * BITS / 32;         // words per gate/up row
+};
+}  // namespace few
+
+// N (up, gate) pairs of a bank: per pair one 4-byte word per lane that,
+// over the wave, holds every scale and bias of both rows (lanes 0-15 up
+// scales, 16-31 gate scales, 32-47 up biases, 48-63 gate biases: 16 words
+// = a row's 32 groups), and the packed chunks lane + 64 i of both rows.
+template <int BITS, int N>
+struct FewPairs {
+  uint4 wu[N][few::Shape<BITS>::CPL], wg[N][few::Shape<BITS>::CPL];
+  uint32_t pw[N];
+};
+
+// The parameter words first (small), then the packed rows in pair order.
+template <int BITS, int N>
+__device__ __forceinline__ void few_load_pairs(FewPairs<BITS, N>& r, const QW& q, size_t up0,
+                                               int lane) {
+  using S = few::Shape<BITS>;
+#pragma unroll
+  for (int pp = 0; pp < N; ++pp) {
+    const size_t row = up0 + pp + ((lane >> 4) & 1) * few::I;
+    const uint16_t* base = (lane < 32 ? q.s : q.b) + row * few::G;
+    r.pw[pp] = reinterpret_cast<const uint32_t*>(base)[lane & 15];
+  }
+#pragma unroll
+  for (int pp = 0; pp < N; ++pp) {
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) {
+      const int ch = lane + 64 * i;
+      r.wu[pp][i] = load16_stream(q.w + (up0 + pp) * S::WPR + ch * 4);
+      r.wg[pp][i] = load16_stream(q.w + (up0 + pp + few::I) * S::WPR + ch * 4);
+    }
+  }
+}
+
+// Keeps the optimiser from converting the codes of every pair once, ahead
+// of a loop over tokens (which held them all as floats and spilled).
+template <int BITS, int N>
+__device__ __forceinline__ void few_opaque(FewPairs<BITS, N>& r) {
+#pragma unroll
+  for (int pp = 0; pp < N; ++pp)
+#pragma unroll
+    for (int i = 0; i < few::Shape<BITS>::CPL; ++i)
+      asm volatile("" : "+v"(r.wu[pp][i].x), "+v"(r.wu[pp][i].y), "+v"(r.wu[pp][i].z),
+                   "+v"(r.wu[pp][i].w), "+v"(r.wg[pp][i].x), "+v"(r.wg[pp][i].y),
+                   "+v"(r.wg[pp][i].z), "+v"(r.wg[pp][i].w));
+}
+
+// One token's x for the gate/up dot: chunks lane + 64 i as loaded (raw),
+// then as floats with the chunk sums.
+template <int BITS>
+struct FewX {
+  uint4 raw[few::Shape<BITS>::CPL][few::Shape<BITS>::VPC / 8];
+  float v[few::Shape<BITS>::CPL][few::Shape<BITS>::VPC];
+  float sum[few::Shape<BITS>::CPL];
+};
+
+template <int BITS>
+__device__ __forceinline__ void few_load_x(uint4 (&raw)[few::Shape<BITS>::CPL]
+                                                      [few::Shape<BITS>::VPC / 8],
+                                           const uint16_t* xt, int lane) {
+  using S = few::Shape<BITS>;
+#pragma unroll
+  for (int i = 0; i < S::CPL; ++i)
+#pragma unroll
+    for (int h = 0; h < S::VPC / 8; ++h) raw[i][h] = load16(xt + (lane + 64 * i) * S::VPC + h * 8);
+}
+
+template <int BITS>
+__device__ __forceinline__ void few_unpack_x(FewX<BITS>& x,
+                                             const uint4 (&raw)[few::Shape<BITS>::CPL]
+                                                               [few::Shape<BITS>::VPC / 8]) {
+  using S = few::Shape<BITS>;
+#pragma unroll
+  for (int i = 0; i < S::CPL; ++i) {
+#pragma unroll
+    for (int h = 0; h < S::VPC / 8; ++h) {
+      const uint4 b = raw[i][h];
+      x.v[i][h * 8 + 0] = bf16_lo(b.x);
+      x.v[i][h * 8 + 1] = bf16_hi(b.x);
+      x.v[i][h * 8 + 2] = bf16_lo(b.y);
+      x.v[i][h * 8 + 3] = bf16_hi(b.y);
+      x.v[i][h * 8 + 4] = bf16_lo(b.z);
+      x.v[i][h * 8 + 5] = bf16_hi(b.z);
+      x.v[i][h * 8 + 6] = bf16_lo(b.w);
+      x.v[i][h * 8 + 7] = bf16_hi(b.w);
+    }
+    x.sum[i] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < S::VPC; ++v) x.sum[i] += x.v[i][v];
+  }
+}
+
+// bf16 value of group g from the parameter word spread over lanes
+// [first, first + 16): word g / 2, half g % 2.
+__device__ __forceinline__ float few_param(uint32_t word, int first, int g) {
+  const uint32_t w = (uint32_t)__shfl((int)word, first + (g >> 1), 64);
+  return __uint_as_float((g & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+
+// One (up, gate) pair's packed chunks.
+template <int BITS>
+struct FewPair {
+  uint4 wu[few::Shape<BITS>::CPL], wg[few::Shape<BITS>::CPL];
+};
+
+template <int BITS>
+__device__ __forceinline__ void few_load_pair(FewPair<BITS>& r, const QW& q, size_t up_row,
+                                              int lane) {
+  using S = few::Shape<BITS>;
+#pragma unroll
+  for (int i = 0; i < S::CPL; ++i) {
+    const int ch = lane + 64 * i;
+    r.wu[i] = load16_stream(q.w + up_row * S::WPR + ch * 4);
+    r.wg[i] = load16_stream(q.w + (up_row + few::I) * S::WPR + ch * 4);
+  }
+}
+
+// bf16 bits of bf16(silu(bf16(gate)) * bf16(up)) of one pair (every lane).
+template <int BITS>
+__device__ __forceinline__ uint32_t few_pair_act(const FewPair<BITS>& r, uint32_t pw,
+                                                 const FewX<BITS>& x, int lane) {
+  using S = few::Shape<BITS>;
+  float au = 0.0f, ag = 0.0f;
+#pragma unroll
+  for (int i = 0; i < S::CPL; ++i) {
+    const int g = ((lane + 64 * i) * S::VPC) >> 6;
+    au += few_param(pw, 0, g) * qdot_chunk<BITS>(r.wu[i], x.v[i]) + few_param(pw, 32, g) * x.sum[i];
+    ag += few_param(pw, 16, g) * qdot_chunk<BITS>(r.wg[i], x.v[i]) + few_param(pw, 48, g) * x.sum[i];
+  }
+  au = wave_sum(au);
+  ag = wave_sum(ag);
+  return f32_to_bf16(silu(round_bf16(ag)) * round_bf16(au));
+}
+
+// SwiGLU activations of N pairs against one token: lane pp < N returns the
+// bf16 bits of pair pp's bf16(silu(bf16(gate)) * bf16(up)).
+template <int BITS, int N>
+__device__ __forceinline__ uint32_t few_pair_acts(const FewPairs<BITS, N>& r,
+                                                  const FewX<BITS>& x, int lane) {
+  using S = few::Shape<BITS>;
+  uint32_t res = 0;
+#pragma unroll
+  for (int pp = 0; pp < N; ++pp) {
+    float au = 0.0f, ag = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) {
+      const int g = ((lane + 64 * i) * S::VPC) >> 6;
+      au += few_param(r.pw[pp], 0, g) * qdot_chunk<BITS>(r.wu[pp][i], x.v[i]) +
+            few_param(r.pw[pp], 32, g) * x.sum[i];
+      ag += few_param(r.pw[pp], 16, g) * qdot_chunk<BITS>(r.wg[pp][i], x.v[i]) +
+            few_param(r.pw[pp], 48, g) * x.sum[i];
+    }
+    au = wave_sum(au);
+    ag = wave_sum(ag);
+    const uint32_t a = f32_to_bf16(silu(round_bf16(ag)) * round_bf16(au));
+    res = lane == pp ? a : res;
+    // one pair at a time: the unpacked codes of later pairs are not hoisted
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return res;
+}
+
+// The router launch's shared-expert role: pairs c0 .. c0 + kSharedPairs - 1
+// for every token (x of all tokens in flight at once).
+template <int BITS>
+__device__ __forceinline__ void few_shared_gate_up(const DecodeArgs& p, int c0, int lane) {
+  using S = few::Shape<BITS>;
+  constexpr int NS = few::kSharedPairs;
+  const int U1 = p.K + 1;
+  uint4 xr[kFewMaxTokens][S::CPL][S::VPC / 8];
+#pragma unroll
+  for (int t = 0; t < kFewMaxTokens; ++t)
+    if (t < p.T) few_load_x<BITS>(xr[t], p.x + (size_t)t * few::H, lane);
+  FewPairs<BITS, NS> pr;
+  few_load_pairs<BITS, NS>(pr, p.sgu, (size_t)c0, lane);
+  uint16_t* act = reinterpret_cast<uint16_t*>(p.act);
+#pragma unroll
+  for (int t = 0; t < kFewMaxTokens; ++t) {
+    if (t < p.T) {
+      FewX<BITS> x;
+      few_unpack_x<BITS>(x, xr[t]);
+      few_opaque(pr);
+      const uint32_t a = few_pair_acts<BITS, NS>(pr, x, lane);
+      if (lane < NS) act[((size_t)t * U1 + p.K) * few::I + c0 + lane] = (uint16_t)a;
+    }
+  }
+}
+
 // ------------------------------------------------------------------ router
 // Ranking, softmax and scores of one token from its bf16-valued logits
 // (lane + 64 i holds expert lane + 64 i; experts >= E are ignored) and the
@@ -170,9 +383,21 @@ __device__ __forceinline__ void q8_gate_partials(const QW& bank, size_t row, con
 // One wave per router row and group of TB tokens (grid.y): the row is
 // streamed once for the group.  The last workgroup of a group ranks its
 // tokens, one wave per token.
-template <int P, int TB>
+template <int P, int TB, int SB>
 __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   static_assert(TB >= 1 && TB <= 4, "one ranking wave per token");
+  const int n_row_blocks = (p.E + p.has_sg + 3) / 4;
+  if constexpr (SB != 0) {
+    // workgroups past the router rows (token group 0 only): the shared
+    // expert's gate/up of every token
+    if ((int)blockIdx.x >= n_row_blocks) {
+      if (blockIdx.y == 0)
+        few_shared_gate_up<SB>(p, ((blockIdx.x - n_row_blocks) * 4 + (threadIdx.x >> 6)) *
+                                      few::kSharedPairs,
+                               threadIdx.x & 63);
+      return;
+    }
+  }
   const int g = blockIdx.y;
   const int t0 = g * TB;
   const int nt = p.T - t0 < TB ? p.T - t0 : TB;
@@ -206,7 +431,7 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev = atomic_add_agent(&p.ctr[g], 1u);
-    s_last = (prev == gridDim.x - 1) ? 1u : 0u;
+    s_last = (prev == (uint32_t)n_row_blocks - 1) ? 1u : 0u;
   }
   __syncthreads();
   if (s_last == 0u || wave >= nt) return;
@@ -857,6 +1082,198 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
   }
 }
 
+// ------------------------------------------------- few tokens: gate/up, down
+// Every wave of these kernels is resident at once, but a wave keeps only a
+// window of its rows in flight (kWindow pairs / units) and issues the next
+// as it consumes one.  With all rows requested at once the memory system
+// served every wave's first row late (measured: the first of 8 pairs landed
+// a median 7.8 us into a 16 us kernel) and the dequantisation ran after the
+// stream instead of under it.
+namespace few {
+constexpr int kWindow = 2;
+}
+
+// One wave per kNP pairs of one routed (token, slot) unit: 64 waves per
+// unit.  Units of the call that chose the same expert share its rows: the
+// first (in token-major order) streams them and computes every member.
+template <int BITS>
+__global__ __launch_bounds__(256) void gate_up_few_kernel(const DecodeArgs p) {
+  constexpr int NP = few::NP;
+  constexpr int D = few::kWindow;
+  const int K = p.K;
+  const int U1 = K + p.has_shared;
+  const int TK = p.T * K;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + wave;
+  const int m = gw / few::kWavesPerUnit;
+  if (m >= TK) return;
+  const int c0 = (gw - m * few::kWavesPerUnit) * NP;
+  const int e = p.idx[m];
+  const int el = lane < TK ? p.idx[lane] : -1;
+  const uint64_t members = __ballot(el == e && lane < TK);
+  if (__builtin_ctzll(members) != m) return;  // an earlier unit streams the rows
+  uint16_t* act = reinterpret_cast<uint16_t*>(p.act);
+  auto act_at = [&](int b) { return ((size_t)(b / K) * U1 + (b % K)) * few::I + c0; };
+  if ((unsigned)e >= (unsigned)p.E) {
+    // caller index outside the bank: zeros, no weight memory touched
+    for (uint64_t mm = members; mm; mm &= mm - 1)
+      if (lane < NP) act[act_at(__builtin_ctzll(mm)) + lane] = 0;
+    return;
+  }
+  const size_t up0 = (size_t)e * 2 * few::I + c0;
+  // every pair's scale/bias word (lanes 0-15 up scales, 16-31 gate scales,
+  // 32-47 up biases, 48-63 gate biases)
+  uint32_t pw[NP];
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+    const size_t row = up0 + pp + ((lane >> 4) & 1) * few::I;
+    pw[pp] = reinterpret_cast<const uint32_t*>((lane < 32 ? p.gu.s : p.gu.b) +
+                                               row * few::G)[lane & 15];
+  }
+  uint4 xr[few::Shape<BITS>::CPL][few::Shape<BITS>::VPC / 8];
+  for (uint64_t mm = members; mm; mm &= mm - 1) {
+    const int b = __builtin_ctzll(mm);
+    few_load_x<BITS>(xr, p.x + (size_t)(b / K) * few::H, lane);  // an L2 hit, first
+    FewPair<BITS> w[NP];
+#pragma unroll
+    for (int pp = 0; pp < D; ++pp) few_load_pair<BITS>(w[pp], p.gu, up0 + pp, lane);
+    FewX<BITS> x;
+    few_unpack_x<BITS>(x, xr);
+    uint32_t res = 0;
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      if (pp + D < NP) few_load_pair<BITS>(w[pp + D], p.gu, up0 + pp + D, lane);
+      issue_fence();
+      const uint32_t a = few_pair_act<BITS>(w[pp], pw[pp], x, lane);
+      res = lane == pp ? a : res;
+      issue_fence();
+    }
+    if (lane < NP) act[act_at(b) + lane] = (uint16_t)res;
+  }
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two bf16 of 8-bit codes q0, q1 (exact: a code has 8 significant bits),
+// packed (q1 << 16 | q0) for v_dot2_f32_bf16.
+__device__ __forceinline__ uint32_t codes_bf16x2(uint32_t w, int pair) {
+  // (v_cvt_f32_ubyte0..3)
+  const float f0 = (float)((w >> (16 * pair)) & 0xFFu);
+  const float f1 = (float)((w >> (16 * pair + 8)) & 0xFFu);
+  return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// One wave per 4 output rows of one token, all its units: lane (r, ch)
+// holds 16-byte chunk ch (16 codes) of rows h0 + r and h0 + 2 + r, and the
+// token's bf16 activations of that chunk (an L2 hit), unit by unit in a
+// window of kWindow units.  Codes become bf16 pairs for v_dot2_f32_bf16
+// against the packed activations.  COMBINE: weighted sum in slot order,
+// gated shared expert, residual; otherwise per-slot rows y[t, j, h].
+template <bool COMBINE>
+__global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
+  constexpr int H = few::H;
+  constexpr int I = few::I;
+  constexpr int NU = kMaxFusedUnits;
+  constexpr int D = few::kWindow;
+  constexpr int WPR = I / 4;  // words per down row
+  constexpr int GD = I / 64;  // groups per down row
+  const int K = p.K;
+  const int U1 = K + p.has_shared;
+  const int units = COMBINE ? U1 : K;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + wave;
+  const int t = gw / few::kDownWavesPerToken;
+  if (t >= p.T) return;
+  const int h0 = (gw - t * few::kDownWavesPerToken) * few::kDownRows;
+  const int r = lane >> 5;
+  const int ch = lane & 31;
+  const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act) + (size_t)t * U1 * I + ch * 16;
+
+  int ev[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) ev[u] = (u < K && u < units) ? p.idx[t * K + u] : 0;
+  uint4 av[NU][2];
+  uint4 wv[NU][2];
+  uint32_t sv[NU][2], bv[NU][2];
+  auto issue = [&](int u) {
+    av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int rp = 0; rp < 2; ++rp) {
+      wv[u][rp] = make_uint4(0, 0, 0, 0);
+      sv[u][rp] = bv[u][rp] = 0;
+    }
+    if (u >= units) return;  // wave-uniform
+    av[u][0] = load16(act + u * I);
+    av[u][1] = load16(act + u * I + 8);
+    const bool sh = u >= K;
+    const int e = ev[u];
+    if (!sh && (unsigned)e >= (unsigned)p.E) return;
+    const QW q = sh ? p.sdn : p.dn;
+#pragma unroll
+    for (int rp = 0; rp < 2; ++rp) {
+      const size_t row = (size_t)e * H + h0 + 2 * rp + r;
+      wv[u][rp] = load16_stream(q.w + row * WPR + ch * 4);
+      sv[u][rp] = q.s[row * GD + (ch >> 2)];
+      bv[u][rp] = q.b[row * GD + (ch >> 2)];
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < D; ++u) issue(u);
+
+  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
+  float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    if (u + D < NU) issue(u + D);
+    issue_fence();
+    if (u < units) {  // wave-uniform
+      const uint32_t aw[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
+                              av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
+      float asum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
+      const float score = COMBINE ? p.scores[t * p.score_stride + u] : 0.0f;
+#pragma unroll
+      for (int rp = 0; rp < 2; ++rp) {
+        const uint32_t ww[4] = {wv[u][rp].x, wv[u][rp].y, wv[u][rp].z, wv[u][rp].w};
+        float dot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          dot = dot2_bf16(codes_bf16x2(ww[k], 0), aw[2 * k], dot);
+          dot = dot2_bf16(codes_bf16x2(ww[k], 1), aw[2 * k + 1], dot);
+        }
+        float y = bf16_to_f32(sv[u][rp]) * dot + bf16_to_f32(bv[u][rp]) * asum;
+        y = round_bf16(segment_sum_fast(y, 32));
+        if constexpr (COMBINE) {
+          acc[rp] += score * y;
+        } else {
+          if (ch == 0)
+            p.out[((size_t)t * K + u) * H + h0 + 2 * rp + r] = (uint16_t)f32_to_bf16(y);
+        }
+      }
+    }
+    issue_fence();
+  }
+  if constexpr (COMBINE) {
+    if (ch == 0) {
+#pragma unroll
+      for (int rp = 0; rp < 2; ++rp) {
+        const int h = h0 + 2 * rp + r;
+        float o = round_bf16(acc[rp]);
+        if (p.residual) o = round_bf16(bf16_to_f32(p.residual[(size_t)t * H + h]) + o);
+        p.out[(size_t)t * H + h] = (uint16_t)f32_to_bf16(o);
+      }
+    }
+  }
+}
+
 // --------------------------------------------------------------------- qmv
 // y[m, n] = x[lhs[m]] . deq(w[rhs[m], n])^T.  Rows of 64/LPR outputs per wave
 // load, where LPR = min(64, chunks per row); CPL chunks per lane.
@@ -985,10 +1402,15 @@ template <int TB>
 static void router_tb(const DecodeArgs& a, hipStream_t s) {
   const int rows = a.E + a.has_sg;
   dim3 grid((rows + 3) / 4, (a.T + TB - 1) / TB);
-  if (a.E <= 256)
-    hipLaunchKernelGGL((router_kernel<4, TB>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((router_kernel<kMaxExperts / 64, TB>), grid, dim3(256), 0, s, a);
+  if (a.few_bits == 8 && a.has_shared) {
+    // plus the shared expert's gate/up (E <= 256 on the few-token path)
+    grid.x += few::kSharedBlocks;
+    hipLaunchKernelGGL((router_kernel<4, TB, 8>), grid, dim3(256), 0, s, a);
+  } else if (a.E <= 256) {
+    hipLaunchKernelGGL((router_kernel<4, TB, 0>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((router_kernel<kMaxExperts / 64, TB, 0>), grid, dim3(256), 0, s, a);
+  }
 }
 
 hipError_t launch_router(const DecodeArgs& a, hipStream_t s) {
@@ -1016,6 +1438,13 @@ static hipError_t gate_up_cpl(const DecodeArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s) {
+  if (a.few_bits == 8) {
+    const int waves = a.T * a.K * few::kWavesPerUnit;
+    hipLaunchKernelGGL(gate_up_few_kernel<8>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       s, a);
+    RMOE_CHECK_LAUNCH();
+    return hipSuccess;
+  }
   const int vpc = bits == 8 ? 16 : 32;
   const int cpl = (a.H / vpc + 63) / 64;
   if (bits == 8) {
@@ -1029,6 +1458,15 @@ hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s) {
 }
 
 hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s) {
+  if (a.few_bits == 8) {
+    const dim3 grid((unsigned)(a.T * few::kDownWavesPerToken / 4));
+    if (combine)
+      hipLaunchKernelGGL(down_few8_kernel<true>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(down_few8_kernel<false>, grid, dim3(256), 0, s, a);
+    RMOE_CHECK_LAUNCH();
+    return hipSuccess;
+  }
   const int vpc = bits == 8 ? 16 : 32;
   const int rpl = 64 / (a.I / vpc);
   const int bpt = (a.H + 4 * rpl - 1) / (4 * rpl);

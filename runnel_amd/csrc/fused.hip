@@ -321,13 +321,6 @@ __device__ __forceinline__ bool shared_gated(const FusedLayer& L, bool has_share
   return has_shared && (RQ ? L.sgq.w != nullptr : L.sgate_w != nullptr);
 }
 
-// Keep the compiler from moving loads or their uses across this point, so
-// that every load of a batch is issued before the first wait on any of them.
-__device__ __forceinline__ void issue_fence() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 // Routing-independent loads of one layer for this wave, in two parts: its
 // router row and its down row of the shared expert (needed first), and its
 // gate/up pairs of the shared expert (unit K).  For a chained layer the

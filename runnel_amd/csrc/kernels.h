@@ -40,6 +40,8 @@ struct DecodeArgs {
   int score_stride;  // K + 1 (the router's scores) or K (caller weights)
   float* act;        // [T, K + has_shared, I]
   uint32_t* ctr;     // [T] zero between calls
+  int few_bits;      // 8: the few-token kernels (act is bf16; the router
+                     // launch also computes the shared expert's gate/up)
   uint16_t* out;     // [T, H] (block) or [T, K, H] (switch)
   const uint16_t* residual;
   int32_t* idx_out;
@@ -67,6 +69,8 @@ constexpr int kMaxFusedRowsPerWave = 1;
 constexpr int kFusedMaxExperts = 256;
 constexpr int kFusedH = 2048;
 constexpr int kFusedI = 512;
+// ---- few-token decode (decode.hip): 2..8 tokens at the shapes above.
+constexpr int kFewMaxTokens = 8;
 
 struct FusedLayer {
   const uint16_t* router_w;
