@@ -1103,7 +1103,11 @@ __global__ __launch_bounds__(256) void gate_up_few_kernel(const DecodeArgs p) {
   const int K = p.K;
   const int U1 = K + p.has_shared;
   const int TK = p.T * K;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform in the compiler's view: the expert ids and scores become
+  // scalar loads, outside the vector-memory counter the rows are waited on
+  // with (a vector load of them issued behind a window of rows made every
+  // wait on it a wait for the whole window)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int gw = blockIdx.x * 4 + wave;
   const int m = gw / few::kWavesPerUnit;
@@ -1186,7 +1190,7 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   const int K = p.K;
   const int U1 = K + p.has_shared;
   const int units = COMBINE ? U1 : K;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // (as in gate/up)
   const int lane = threadIdx.x & 63;
   const int gw = blockIdx.x * 4 + wave;
   const int t = gw / few::kDownWavesPerToken;
@@ -1196,29 +1200,53 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   const int ch = lane & 31;
   const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act) + (size_t)t * U1 * I + ch * 16;
 
-  int ev[NU];
+  // Experts of the token's slots; an index outside the bank (a caller's)
+  // reads expert 0 and contributes zero.  Loads are issued without branches
+  // around them: a select between a loaded value and a constant made the
+  // compiler convert the loaded value at once, waiting for the whole window.
+  // Units past the call's last (K + shared < 9) re-read the last unit's
+  // rows (cache hits) and are not computed: no branch around any load
+  // (paths that reach a wait with different loads in flight made the
+  // compiler wait for all of them).
+  int ev[NU], ua[NU];
+  bool ush[NU];
+  uint32_t bad = 0;
 #pragma unroll
-  for (int u = 0; u < NU; ++u) ev[u] = (u < K && u < units) ? p.idx[t * K + u] : 0;
+  for (int u = 0; u < NU; ++u) {
+    if (u < units || u == 0) {
+      int e = 0;
+      if (u < K) {
+        e = p.idx[t * K + u];
+        const bool ok = (unsigned)e < (unsigned)p.E;
+        bad |= ok ? 0u : 1u << u;
+        e = ok ? e : 0;
+      }
+      ev[u] = e;
+      ush[u] = u >= K;
+      ua[u] = u;
+    } else {
+      ev[u] = ev[u - 1];
+      ush[u] = ush[u - 1];
+      ua[u] = ua[u - 1];
+    }
+  }
+  const QW dn = p.dn, sdn = p.sdn;
+  // the combine weights, loaded ahead of the rows (loaded in the loop, a
+  // wait for one was a wait for the window behind it)
+  float score[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+    score[u] = (COMBINE && u < units) ? p.scores[t * p.score_stride + u] : 0.0f;
   uint4 av[NU][2];
   uint4 wv[NU][2];
   uint32_t sv[NU][2], bv[NU][2];
   auto issue = [&](int u) {
-    av[u][0] = av[u][1] = make_uint4(0, 0, 0, 0);
+    av[u][0] = load16(act + ua[u] * I);
+    av[u][1] = load16(act + ua[u] * I + 8);
+    const QW& q = ush[u] ? sdn : dn;
 #pragma unroll
     for (int rp = 0; rp < 2; ++rp) {
-      wv[u][rp] = make_uint4(0, 0, 0, 0);
-      sv[u][rp] = bv[u][rp] = 0;
-    }
-    if (u >= units) return;  // wave-uniform
-    av[u][0] = load16(act + u * I);
-    av[u][1] = load16(act + u * I + 8);
-    const bool sh = u >= K;
-    const int e = ev[u];
-    if (!sh && (unsigned)e >= (unsigned)p.E) return;
-    const QW q = sh ? p.sdn : p.dn;
-#pragma unroll
-    for (int rp = 0; rp < 2; ++rp) {
-      const size_t row = (size_t)e * H + h0 + 2 * rp + r;
+      const size_t row = (size_t)ev[u] * H + h0 + 2 * rp + r;
       wv[u][rp] = load16_stream(q.w + row * WPR + ch * 4);
       sv[u][rp] = q.s[row * GD + (ch >> 2)];
       bv[u][rp] = q.b[row * GD + (ch >> 2)];
@@ -1239,7 +1267,6 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
       float asum = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
-      const float score = COMBINE ? p.scores[t * p.score_stride + u] : 0.0f;
 #pragma unroll
       for (int rp = 0; rp < 2; ++rp) {
         const uint32_t ww[4] = {wv[u][rp].x, wv[u][rp].y, wv[u][rp].z, wv[u][rp].w};
@@ -1249,10 +1276,14 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
           dot = dot2_bf16(codes_bf16x2(ww[k], 0), aw[2 * k], dot);
           dot = dot2_bf16(codes_bf16x2(ww[k], 1), aw[2 * k + 1], dot);
         }
-        float y = bf16_to_f32(sv[u][rp]) * dot + bf16_to_f32(bv[u][rp]) * asum;
+        // converted here, not where they are loaded (which waited for them)
+        uint32_t sw = sv[u][rp], bw = bv[u][rp];
+        asm volatile("" : "+v"(sw), "+v"(bw));
+        float y = bf16_to_f32(sw) * dot + bf16_to_f32(bw) * asum;
         y = round_bf16(segment_sum_fast(y, 32));
+        y = (bad >> u) & 1u ? 0.0f : y;
         if constexpr (COMBINE) {
-          acc[rp] += score * y;
+          acc[rp] += score[u] * y;
         } else {
           if (ch == 0)
             p.out[((size_t)t * K + u) * H + h0 + 2 * rp + r] = (uint16_t)f32_to_bf16(y);
