@@ -30,11 +30,14 @@ namespace few {
 constexpr int H = kFusedH;
 constexpr int I = kFusedI;
 constexpr int G = H / 64;                 // groups per gate/up row (32)
-constexpr int NP = 8;                     // gate/up pairs per wave
-constexpr int kWavesPerUnit = I / NP;     // 64
+// gate/up pairs per wave: small waves, many per SIMD (4 tokens through 40
+// layers from HBM, us per layer call: 8 pairs 42.0, 4 pairs 34.7, 2 pairs 30.5)
+constexpr int NP = 2;
+constexpr int kWavesPerUnit = I / NP;
 constexpr int kSharedPairs = 2;           // router launch: shared pairs per wave
 constexpr int kSharedBlocks = I / (4 * kSharedPairs);  // 64
-constexpr int kDownRows = 4;              // down rows per wave
+constexpr int kDownRowPairs = 2;          // down: row pairs per wave
+constexpr int kDownRows = 2 * kDownRowPairs;
 constexpr int kDownWavesPerToken = H / kDownRows;      // 512
 template <int BITS>
 struct Shape {
@@ -1084,16 +1087,16 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
 
 // ------------------------------------------------- few tokens: gate/up, down
 // Every wave of these kernels is resident at once, but a wave keeps only a
-// window of its rows in flight (kWindow pairs / units) and issues the next
-// as it consumes one.  With all rows requested at once the memory system
+// window of its rows in flight (kWindow pairs / units beyond the one it
+// computes) and issues the next as it consumes one.  With all rows requested at once the memory system
 // served every wave's first row late (measured: the first of 8 pairs landed
 // a median 7.8 us into a 16 us kernel) and the dequantisation ran after the
 // stream instead of under it.
 namespace few {
-constexpr int kWindow = 2;
+constexpr int kWindow = 1;
 }
 
-// One wave per kNP pairs of one routed (token, slot) unit: 64 waves per
+// One wave per NP pairs of one routed (token, slot) unit: I / NP waves per
 // unit.  Units of the call that chose the same expert share its rows: the
 // first (in token-major order) streams them and computes every member.
 template <int BITS>
@@ -1173,8 +1176,8 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// One wave per 4 output rows of one token, all its units: lane (r, ch)
-// holds 16-byte chunk ch (16 codes) of rows h0 + r and h0 + 2 + r, and the
+// One wave per kDownRows output rows of one token, all its units: lane
+// (r, ch) holds 16-byte chunk ch (16 codes) of rows h0 + 2 rp + r, and the
 // token's bf16 activations of that chunk (an L2 hit), unit by unit in a
 // window of kWindow units.  Codes become bf16 pairs for v_dot2_f32_bf16
 // against the packed activations.  COMBINE: weighted sum in slot order,
@@ -1185,6 +1188,7 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   constexpr int I = few::I;
   constexpr int NU = kMaxFusedUnits;
   constexpr int D = few::kWindow;
+  constexpr int RP = few::kDownRowPairs;
   constexpr int WPR = I / 4;  // words per down row
   constexpr int GD = I / 64;  // groups per down row
   const int K = p.K;
@@ -1238,14 +1242,14 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   for (int u = 0; u < NU; ++u)
     score[u] = (COMBINE && u < units) ? p.scores[t * p.score_stride + u] : 0.0f;
   uint4 av[NU][2];
-  uint4 wv[NU][2];
-  uint32_t sv[NU][2], bv[NU][2];
+  uint4 wv[NU][RP];
+  uint32_t sv[NU][RP], bv[NU][RP];
   auto issue = [&](int u) {
     av[u][0] = load16(act + ua[u] * I);
     av[u][1] = load16(act + ua[u] * I + 8);
     const QW& q = ush[u] ? sdn : dn;
 #pragma unroll
-    for (int rp = 0; rp < 2; ++rp) {
+    for (int rp = 0; rp < RP; ++rp) {
       const size_t row = (size_t)ev[u] * H + h0 + 2 * rp + r;
       wv[u][rp] = load16_stream(q.w + row * WPR + ch * 4);
       sv[u][rp] = q.s[row * GD + (ch >> 2)];
@@ -1256,7 +1260,7 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   for (int u = 0; u < D; ++u) issue(u);
 
   constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
-  float acc[2] = {0.0f, 0.0f};
+  float acc[RP] = {};
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     if (u + D < NU) issue(u + D);
@@ -1268,7 +1272,7 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
 #pragma unroll
-      for (int rp = 0; rp < 2; ++rp) {
+      for (int rp = 0; rp < RP; ++rp) {
         const uint32_t ww[4] = {wv[u][rp].x, wv[u][rp].y, wv[u][rp].z, wv[u][rp].w};
         float dot = 0.0f;
 #pragma unroll
@@ -1295,7 +1299,7 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   if constexpr (COMBINE) {
     if (ch == 0) {
 #pragma unroll
-      for (int rp = 0; rp < 2; ++rp) {
+      for (int rp = 0; rp < RP; ++rp) {
         const int h = h0 + 2 * rp + r;
         float o = round_bf16(acc[rp]);
         if (p.residual) o = round_bf16(bf16_to_f32(p.residual[(size_t)t * H + h]) + o);
