@@ -444,9 +444,11 @@ def main():
         out["few_token"] = run_few_tokens(torch, res["stack"], 4)
     if not args.no_prefill:
         # prefill figures of the same build (one layer per call, HIP events)
+        # enough warm-up calls for the clocks to settle: three back-to-back
+        # rounds of 13 calls measured 904, 815 and 792 us at 8192 tokens
         out["prefill"] = {
-            "512 tokens 8-bit": run_prefill(torch, 512, 8, False, 20, 3),
-            "8192 tokens 4-bit zipf": run_prefill(torch, 8192, 4, True, 10, 2),
+            "512 tokens 8-bit": run_prefill(torch, 512, 8, False, 20, 40),
+            "8192 tokens 4-bit zipf": run_prefill(torch, 8192, 4, True, 20, 30),
         }
     if not args.no_cpu_baseline:
         from oracle.moe_ref import f32_to_bf16

@@ -13,7 +13,8 @@
 //                           descriptor per m-tile.
 //   prefill_gemm_kernel     MODE 0 (gate/up): one (m-tile, n-tile of [up;
 //                           gate] pairs) per workgroup; the x rows of the
-//                           tile staged in LDS, every wave streams its own
+//                           tile staged in LDS (128-row tiles: by LDS-DMA,
+//                           three stages ahead), every wave streams its own
 //                           up and gate weight rows straight from HBM into
 //                           registers, dequantises them to bf16 (fl32(q*s +
 //                           b) rounded to nearest even) and feeds
@@ -26,10 +27,11 @@
 //                           the gated shared row, residual, bf16.
 //
 // Tiles are 32 rows (short prefill: memory bound, few rows per expert) or
-// 128 rows (long prefill: matrix-core bound).  A workgroup is 8 waves, 4 for
-// the short gate/up tiles (at least two waves per SIMD: a single wave per
-// SIMD issues vector instructions too slowly to keep the dequantisation
-// beside the MFMAs); each wave owns 32 weight columns of the tile.
+// 128 rows (long prefill: matrix-core bound).  32-row tiles: a workgroup is
+// 8 waves, 4 for the gate/up tiles, each wave owning 32 weight columns;
+// 128-row tiles: 4 waves of 64 columns, two workgroups per CU (at least two
+// waves per SIMD either way: a single wave per SIMD issues vector
+// instructions too slowly to keep the dequantisation beside the MFMAs).
 //
 // MFMA operand layout (16x16x32 bf16, checked on the device): lane l holds
 // A row l % 16 and B column l % 16, k = 8 (l / 16) + [0, 8); D column l % 16,
