@@ -361,6 +361,8 @@ def main():
                     help="decode40: the bench line; the prefill workloads and few "
                          "(2, 4 and 7 tokens through the 40-layer stack) print their "
                          "own line (exploration and profiling)")
+    ap.add_argument("--few-tokens", default="2,4,7",
+                    help="token counts of --workload few (comma-separated)")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the prefill figures appended to the decode line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -382,8 +384,8 @@ def main():
         stack = build_stack(args.layers, 8)
         torch.cuda.synchronize()
         print(json.dumps({"workload": "few", "runs": [
-            run_few_tokens(torch, stack, T, args.steps, args.warmup) for T in (2, 4, 7)]}),
-            flush=True)
+            run_few_tokens(torch, stack, int(T), args.steps, args.warmup)
+            for T in args.few_tokens.split(",")]}), flush=True)
         return 0
     if args.workload != "decode40":
         tokens, bits, skewed = (512, 8, False) if args.workload == "prefill512" else (8192, 4, True)
