@@ -530,134 +530,188 @@ __global__ __launch_bounds__(256) void router_split_kernel(const DecodeArgs p, u
 typedef __bf16 bf16x8_r __attribute__((ext_vector_type(8)));
 typedef float f32x4_r __attribute__((ext_vector_type(4)));
 
-// Matrix-core router logits: a workgroup takes 16 TB tokens x 64 experts and
-// splits K over its KS waves (wave w: chunks [w n / KS, (w + 1) n / KS) of
-// 64 values, D chunks of loads in flight); lane (col, g) holds A row / B
-// column `col` and k = 16 g + [0, 16) of each chunk.  The waves' partial
-// tiles meet in LDS and are added in wave order, after the sums already in
-// `logits` for ACC (the second plane of a split gate).  Splitting K keeps
-// every wave's chain of dependent loads short: the tile of one wave walking
-// all of K waited for a memory round trip every few chunks.  WNORM: the
-// workgroups of the first token tile also write the bound ||w_e||_2 (1 +
-// 2^-10) of their 64 router rows into wnorm from the rows they stream (the
-// padding covers any order of the fp32 sum of squares).
-template <int TB, int KS, int D, bool ACC, bool WNORM>
-__global__ __launch_bounds__(64 * KS) void router_logits_kernel(const DecodeArgs p,
-                                                                float* wnorm) {
-  const int wave = threadIdx.x >> 6;
+// Matrix-core router logits: a workgroup computes BT tokens x BE experts over
+// the whole of K.  Each stage of 64 k values of its BT token rows and BE
+// router rows (128 bytes of each) arrives in LDS by LDS-DMA, eight lanes per
+// row so that every load instruction fetches whole 128-byte lines; NB stage
+// buffers, NB - 1 stages in flight.  Wave (wm, wn) of the WM x WN grid
+// multiplies its (BT / WM) x (BE / WN) block from LDS fragments.  Loading
+// the fragments straight into registers (16 rows x 64 bytes per instruction)
+// took 35 us at 8192 tokens against 21 us for this kernel (13.5 against 11.7
+// at 512 tokens; event-timed, 5.5 us of launch included).
+//
+// Stage layout (as the grouped GEMM's): row r holds 8 slots of 16 bytes,
+// slot sl at position 8 r + (sl ^ f(r)), f(r) = (r & 7) ^ ((r >> 3) & 1), so
+// the 16-row operand reads fall on distinct bank groups.  Slot 2 kg + j holds
+// the 8 k values lane group kg feeds to k-step j; A and B share the layout,
+// so the products pair equal k.  The waits are counted: every stage issues
+// the same ND DMAs per wave (stages past the end reload the last one into a
+// buffer nobody reads), so NB - 2 stages' loads may stay in flight when a
+// stage's own copy is needed.
+//
+// ACC adds the sums already in `logits` (the second plane of a split gate).
+// WNORM: the first token tile's workgroups also write the bound
+// ||w_e||_2 (1 + 2^-10) of their router rows into wnorm from the fragments
+// they read (the padding covers any order of the fp32 sum of squares).
+__device__ __forceinline__ int stage_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <int BT, int BE, int WM, int WN>
+struct LogitsTile {
+  static constexpr int WAVES = WM * WN, ROWS = BT + BE, NI = ROWS / 8, ND = NI / WAVES;
+  static constexpr int MBW = BT / WM / 16, CBW = BE / WN / 16;
+  static_assert(NI % WAVES == 0 && MBW >= 1 && CBW >= 1, "tile shape");
+  static constexpr int vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+};
+
+template <int BT, int BE, int WM, int WN, bool WNORM>
+__device__ __forceinline__ void logits_stage(
+    const uint16_t* __restrict__ buf, const int (&rd)[2], int arow0, int brow0,
+    f32x4_r (&acc)[LogitsTile<BT, BE, WM, WN>::MBW][LogitsTile<BT, BE, WM, WN>::CBW],
+    float (&ss)[LogitsTile<BT, BE, WM, WN>::CBW], bool norms) {
+  using C = LogitsTile<BT, BE, WM, WN>;
+  const char* b = reinterpret_cast<const char*>(buf);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    u32x4 bf[C::CBW];
+#pragma unroll
+    for (int cb = 0; cb < C::CBW; ++cb)
+      bf[cb] = *reinterpret_cast<const u32x4*>(b + (brow0 + cb * 16) * 128 + rd[j]);
+    if (WNORM && norms) {
+#pragma unroll
+      for (int cb = 0; cb < C::CBW; ++cb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ss[cb] = fmaf(bf16_lo(bf[cb][i]), bf16_lo(bf[cb][i]), ss[cb]);
+          ss[cb] = fmaf(bf16_hi(bf[cb][i]), bf16_hi(bf[cb][i]), ss[cb]);
+        }
+    }
+#pragma unroll
+    for (int mb = 0; mb < C::MBW; ++mb) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(b + (arow0 + mb * 16) * 128 + rd[j]);
+#pragma unroll
+      for (int cb = 0; cb < C::CBW; ++cb)
+        acc[mb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_r, a), __builtin_bit_cast(bf16x8_r, bf[cb]), acc[mb][cb], 0,
+            0, 0);
+    }
+  }
+}
+
+template <int BT, int BE, int WM, int WN, int NB, bool ACC, bool WNORM>
+__device__ __forceinline__ void router_logits_body(const DecodeArgs& p, float* wnorm,
+                                                   uint16_t* __restrict__ s0,
+                                                   uint16_t* __restrict__ s1,
+                                                   uint16_t* __restrict__ s2,
+                                                   uint16_t* __restrict__ s3) {
+  using C = LogitsTile<BT, BE, WM, WN>;
+  uint16_t* const sb[4] = {s0, s1, s2, s3};
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int col = lane & 15;
-  const int g = lane >> 4;
-  const int t0 = blockIdx.x * 16 * TB;
-  const int e0 = blockIdx.y * 64;
-  const uint16_t* xa[TB];
+  const int kg = lane >> 4;
+  const int t0 = blockIdx.x * BT, e0 = blockIdx.y * BE;
+  const int trows = min(BT, p.T - t0);
+  const int H = p.H;
+  // resources based at the tile's first token / router row (offsets stay 32-bit)
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (size_t)t0 * H), (short)0, trows * H * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.router_w + (size_t)e0 * H), (short)0, BE * H * 2, 0x00020000);
+  // DMA ii of this wave covers stage rows 8 i .. 8 i + 7, i = wave + WAVES ii:
+  // lane l fetches the slot that belongs at position l & 7 of row 8 i + l / 8
+  uint32_t src[C::ND];
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
-    xa[tb] = p.x + (size_t)min(t0 + tb * 16 + col, p.T - 1) * p.H + g * 16;
-  const uint16_t* wb[4];
+  for (int ii = 0; ii < C::ND; ++ii) {
+    const int i = wave + C::WAVES * ii;
+    const int r = 8 * i + (lane >> 3);
+    const int sl = (lane & 7) ^ stage_swizzle(r);
+    const int row = 8 * i >= BT ? r - BT : min(r, trows - 1);  // tokens past the end: the last
+    src[ii] = ((uint32_t)row * H + sl * 8) * 2;
+  }
+  const int wm = wave % WM, wn = wave / WM;
+  const int arow0 = wm * (BT / WM), brow0 = BT + wn * (BE / WN);
+  int rd[2];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) wb[cb] = p.router_w + (size_t)(e0 + cb * 16 + col) * p.H + g * 16;
-  f32x4_r acc[TB][4];
+  for (int j = 0; j < 2; ++j)
+    rd[j] = ((lane & 15) * 8 + ((2 * kg + j) ^ stage_swizzle(lane & 15))) * 16;
+  f32x4_r acc[C::MBW][C::CBW];
 #pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
+  for (int mb = 0; mb < C::MBW; ++mb)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[tb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
-  const bool norms = WNORM && blockIdx.x == 0;
-  float ss[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's squares of rows cb
-  const int per = p.H / 64 / KS;  // the host checks H % (64 KS) == 0
-  const int c_begin = wave * per;
-  const int c_end = c_begin + per;
-  for (int c0 = c_begin; c0 < c_end; c0 += D) {
-    u32x4 a[D][TB][2], b[D][4][2];
+    for (int cb = 0; cb < C::CBW; ++cb) acc[mb][cb] = f32x4_r{0.f, 0.f, 0.f, 0.f};
+  float ss[C::CBW];
 #pragma unroll
-    for (int u = 0; u < D; ++u) {
-      if (c0 + u < c_end) {
+  for (int cb = 0; cb < C::CBW; ++cb) ss[cb] = 0.f;
+  const bool norms = WNORM && blockIdx.x == 0 && wm == 0;
+  const int nst = H / 64;
+  auto dma = [&](uint16_t* buf, int c) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+    for (int ii = 0; ii < C::ND; ++ii) {
+      const int i = wave + C::WAVES * ii;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          8 * i >= BT ? rb : ra, (__attribute__((address_space(3))) void*)(buf + i * 512), 16,
+          src[ii], c * 128, 0, 0);
+    }
+  };
 #pragma unroll
-          for (int tb = 0; tb < TB; ++tb)
-            a[u][tb][j] = *reinterpret_cast<const u32x4*>(xa[tb] + (c0 + u) * 64 + 8 * j);
+  for (int q = 0; q < NB - 1; ++q) {
+    __builtin_amdgcn_sched_barrier(0);
+    dma(sb[q], min(q, nst - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(C::vmcnt((NB - 2) * C::ND));
+  __builtin_amdgcn_s_barrier();
+  for (int c = 0; c < nst; c += NB) {
 #pragma unroll
-          for (int cb = 0; cb < 4; ++cb)
-            b[u][cb][j] = *reinterpret_cast<const u32x4*>(wb[cb] + (c0 + u) * 64 + 8 * j);
+    for (int q = 0; q < NB; ++q) {
+      if (c + q < nst) {
+        __builtin_amdgcn_sched_barrier(0);
+        dma(sb[(q + NB - 1) % NB], min(c + q + NB - 1, nst - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        logits_stage<BT, BE, WM, WN, WNORM>(sb[q], rd, arow0, brow0, acc, ss, norms);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(C::vmcnt((NB - 2) * C::ND));
+        __builtin_amdgcn_s_barrier();
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(C::vmcnt(0));  // the DMAs past the end have landed
+  if (WNORM && norms) {
+#pragma unroll
+    for (int cb = 0; cb < C::CBW; ++cb) {
+      float v = ss[cb];
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      if (kg == 0)
+        wnorm[e0 + brow0 - BT + cb * 16 + (lane & 15)] = sqrtf(v) * (1.0f + 1.0f / 1024.0f);
+    }
+  }
+  // lane (col, kg) of block (mb, cb) holds tokens 4 kg + [0, 4) of expert col
+#pragma unroll
+  for (int mb = 0; mb < C::MBW; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < C::CBW; ++cb) {
+      const int e = e0 + brow0 - BT + cb * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + arow0 + mb * 16 + 4 * kg + i;
+        if (t < p.T) {
+          float* o = p.logits + (size_t)t * (p.E + 1) + e;
+          *o = ACC ? *o + acc[mb][cb][i] : acc[mb][cb][i];
         }
       }
     }
-    if (norms) {
-#pragma unroll
-      for (int u = 0; u < D; ++u)
-        if (c0 + u < c_end)
-#pragma unroll
-          for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const u32x4 w = b[u][cb][j];
-              const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                ss[cb] = fmaf(bf16_lo(ww[i]), bf16_lo(ww[i]), ss[cb]);
-                ss[cb] = fmaf(bf16_hi(ww[i]), bf16_hi(ww[i]), ss[cb]);
-              }
-            }
-    }
-#pragma unroll
-    for (int u = 0; u < D; ++u) {
-      if (c0 + u < c_end) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-              acc[tb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  __builtin_bit_cast(bf16x8_r, a[u][tb][j]),
-                  __builtin_bit_cast(bf16x8_r, b[u][cb][j]), acc[tb][cb], 0, 0, 0);
-      }
-    }
-  }
-  __shared__ f32x4_r s_part[KS][TB * 4][64];
-  __shared__ float s_ss[WNORM ? KS : 1][4][64];
-#pragma unroll
-  for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) s_part[wave][tb * 4 + cb][lane] = acc[tb][cb];
-  if (norms) {
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) s_ss[wave][cb][lane] = ss[cb];
-  }
-  __syncthreads();
-  if (norms && wave == KS - 1) {
-    // lane l: row cb = l / 16, column col = l % 16, summed over the four
-    // k groups and the waves
-    const int cb = lane >> 4;
-    float n2 = 0.0f;
-#pragma unroll
-    for (int w = 0; w < KS; ++w)
-#pragma unroll
-      for (int gg = 0; gg < 4; ++gg) n2 += s_ss[w][cb][gg * 16 + (lane & 15)];
-    wnorm[e0 + lane] = sqrtf(n2) * (1.0f + 1.0f / 1024.0f);
-  }
-  // tile blocks (tb, cb) are summed by waves in turn
-  for (int blk = wave; blk < TB * 4; blk += KS) {
-    const int tb = blk >> 2;
-    const int cb = blk & 3;
-    const int e = e0 + cb * 16 + col;
-    f32x4_r r = f32x4_r{0.f, 0.f, 0.f, 0.f};
-    if constexpr (ACC) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t0 + tb * 16 + 4 * g + i;
-        if (t < p.T) r[i] = p.logits[(size_t)t * (p.E + 1) + e];
-      }
-    }
-#pragma unroll
-    for (int w = 0; w < KS; ++w) r += s_part[w][blk][lane];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + tb * 16 + 4 * g + i;
-      if (t < p.T) p.logits[(size_t)t * (p.E + 1) + e] = r[i];
-    }
-  }
+}
+
+template <int BT, int BE, int WM, int WN, int NB, bool ACC, bool WNORM>
+__global__ __launch_bounds__(64 * WM * WN) void router_logits_kernel(const DecodeArgs p,
+                                                                     float* wnorm) {
+  static_assert(NB >= 3 && NB <= 4, "stage buffers");
+  using C = LogitsTile<BT, BE, WM, WN>;
+  __shared__ __attribute__((aligned(16))) uint16_t s0[C::ROWS * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t s1[C::ROWS * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t s2[C::ROWS * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t s3[NB > 3 ? C::ROWS * 64 : 8];
+  router_logits_body<BT, BE, WM, WN, NB, ACC, WNORM>(p, wnorm, s0, s1, s2, s3);
 }
 
 // The router contract's dot of one token row (held as xv, chunk lane + 64 c
@@ -1385,12 +1439,21 @@ bool router_mfma_eligible(int E, int H) {
   return E % 64 == 0 && E <= 256 && H % 512 == 0 && H <= 4096;
 }
 
+// 64 x 64 tiles (two workgroups of four waves per CU) from 4096 tokens on,
+// 32 x 32 below, where 64-token tiles leave most CUs idle: at 512 tokens
+// 11.7 against 17.3 us, at 8192 tokens 21.2 against 32.2 (event-timed).
+template <bool ACC, bool WNORM>
+static void launch_logits(const DecodeArgs& a, float* wnorm, hipStream_t s) {
+  if (a.T >= 4096)
+    hipLaunchKernelGGL((router_logits_kernel<64, 64, 2, 2, 3, ACC, WNORM>),
+                       dim3((a.T + 63) / 64, a.E / 64), dim3(256), 0, s, a, wnorm);
+  else
+    hipLaunchKernelGGL((router_logits_kernel<32, 32, 2, 2, 4, ACC, WNORM>),
+                       dim3((a.T + 31) / 32, a.E / 32), dim3(256), 0, s, a, wnorm);
+}
+
 hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split,
                               hipStream_t s) {
-  // 64-token tiles from 4096 tokens on (each router row read once per 64
-  // tokens), K over 4 waves; shorter prefills 16-token tiles, K over 8 waves
-  const dim3 g16((a.T + 15) / 16, a.E / 64), g64((a.T + 63) / 64, a.E / 64);
-  const bool wide = a.T >= 4096;
   if (a.rq8) {
     // logits over the hi plane, then continued over the lo plane
     hipLaunchKernelGGL(router_split_kernel, dim3((a.E + 3) / 4), dim3(256), 0, s, a, split,
@@ -1398,27 +1461,13 @@ hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split
     DecodeArgs hi = a, lo = a;
     hi.router_w = split;
     lo.router_w = split + (size_t)a.E * a.H;
-    if (wide) {
-      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false, false>), g64, dim3(256), 0, s, hi,
-                         nullptr);
-      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, true, false>), g64, dim3(256), 0, s, lo,
-                         nullptr);
-    } else {
-      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false, false>), g16, dim3(512), 0, s, hi,
-                         nullptr);
-      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, true, false>), g16, dim3(512), 0, s, lo,
-                         nullptr);
-    }
+    launch_logits<false, false>(hi, nullptr, s);
+    launch_logits<true, false>(lo, nullptr, s);
     hipLaunchKernelGGL(router_select_kernel<1>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   } else {
     // the row norms come from the first token tile's workgroups
-    if (wide)
-      hipLaunchKernelGGL((router_logits_kernel<4, 4, 2, false, true>), g64, dim3(256), 0, s, a,
-                         wnorm);
-    else
-      hipLaunchKernelGGL((router_logits_kernel<1, 8, 4, false, true>), g16, dim3(512), 0, s, a,
-                         wnorm);
+    launch_logits<false, true>(a, wnorm, s);
     hipLaunchKernelGGL(router_select_kernel<0>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
                        (const float*)wnorm);
   }
