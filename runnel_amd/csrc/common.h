@@ -212,11 +212,6 @@ __device__ __forceinline__ float qdot_chunk(const uint4 w, const float* v) {
   return acc;
 }
 
-// One 16-byte chunk (16 codes) of an 8-bit MLX-affine gate row folded into
-// a router lane's partial, in the fixed order of the quantized router
-// contract: qa = sum q_i v_i and xs = sum v_i, each sequential from +0 (the
-// products are exact), then acc = fma(qa, s, acc), acc = fma(xs, b, acc)
-// with the chunk's group scale and bias.
 // Keep the compiler from moving loads or their uses across this point, so
 // that every load of a batch is issued before the first wait on any of them.
 __device__ __forceinline__ void issue_fence() {
@@ -224,6 +219,11 @@ __device__ __forceinline__ void issue_fence() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// One 16-byte chunk (16 codes) of an 8-bit MLX-affine gate row folded into
+// a router lane's partial, in the fixed order of the quantized router
+// contract: qa = sum q_i v_i and xs = sum v_i, each sequential from +0 (the
+// products are exact), then acc = fma(qa, s, acc), acc = fma(xs, b, acc)
+// with the chunk's group scale and bias.
 __device__ __forceinline__ float qgate_chunk(float acc, const uint4 w, const float* v, float s,
                                              float b) {
   const float qa = qdot_chunk<8>(w, v);

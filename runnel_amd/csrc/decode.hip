@@ -714,33 +714,6 @@ __global__ __launch_bounds__(64 * WM * WN) void router_logits_kernel(const Decod
   router_logits_body<BT, BE, WM, WN, NB, ACC, WNORM>(p, wnorm, s0, s1, s2, s3);
 }
 
-// The router contract's dot of one token row (held as xv, chunk lane + 64 c
-// per lane) with one weight row.
-template <int XC>
-__device__ __forceinline__ float contract_dot(const uint4 (&xv)[XC], int nxc,
-                                              const uint16_t* w) {
-  const int lane = threadIdx.x & 63;
-  uint4 wv[XC];
-#pragma unroll
-  for (int c = 0; c < XC; ++c)
-    if (c < nxc) wv[c] = load16(w + (lane + 64 * c) * 8);
-  float acc = 0.0f;
-#pragma unroll
-  for (int c = 0; c < XC; ++c) {
-    if (c < nxc) {
-      acc = fmaf(bf16_lo(xv[c].x), bf16_lo(wv[c].x), acc);
-      acc = fmaf(bf16_hi(xv[c].x), bf16_hi(wv[c].x), acc);
-      acc = fmaf(bf16_lo(xv[c].y), bf16_lo(wv[c].y), acc);
-      acc = fmaf(bf16_hi(xv[c].y), bf16_hi(wv[c].y), acc);
-      acc = fmaf(bf16_lo(xv[c].z), bf16_lo(wv[c].z), acc);
-      acc = fmaf(bf16_hi(xv[c].z), bf16_hi(wv[c].z), acc);
-      acc = fmaf(bf16_lo(xv[c].w), bf16_lo(wv[c].w), acc);
-      acc = fmaf(bf16_hi(xv[c].w), bf16_hi(wv[c].w), acc);
-    }
-  }
-  return wave_sum(acc);
-}
-
 __device__ __forceinline__ uint32_t f32_order_key(float v) {
   const uint32_t u = __float_as_uint(v);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -749,62 +722,153 @@ __device__ __forceinline__ float f32_from_order_key(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// The quantized router contract's dot of one token row (held as xv: chunk
-// lane + 64 i in xv[2 i], xv[2 i + 1]) with row `row` of an 8-bit gate bank.
-__device__ __forceinline__ float q8_contract_dot(const uint4 (&xv)[8], const QW& bank, size_t row,
-                                                 int H) {
-  const int lane = threadIdx.x & 63;
-  const int chunks = H >> 4;
-  uint4 wv[4];
-  uint32_t sv[4], bv[4];
+// One gate row re-checked in the router contract's order, as this lane
+// walks it: bf16 gate, 16-byte piece c = chunk lane + 64 c (8 values);
+// 8-bit gate, chunk lane + 64 i (16 codes) with its group's scale and bias.
+// The token row xv has the same layout (8-bit: chunk i in xv[2 i],
+// xv[2 i + 1]).  XC pieces of the token row cover H <= 512 XC.
+template <int RQ, int XC>
+struct CheckRow {
+  static constexpr int NW = RQ ? XC / 2 : XC;
+  uint4 w[NW];
+  uint32_t s[RQ ? NW : 1], b[RQ ? NW : 1];
+};
+
+// The loads of one row, none of them conditional (pieces past the row's end
+// reload its first piece and the dot skips them), so that the compiler
+// can count the loads in flight and wait for this row alone.
+template <int RQ, int XC>
+__device__ __forceinline__ void check_load(CheckRow<RQ, XC>& r, const uint16_t* wrow,
+                                           const QW& bank, size_t row, int H, int lane) {
+  if constexpr (RQ) {
+    const int chunks = H >> 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ch = lane + 64 * i;
-    if (ch < chunks) {
-      wv[i] = load16(bank.w + row * (size_t)(H >> 2) + ch * 4);
-      sv[i] = bank.s[row * (size_t)(H >> 6) + (ch >> 2)];
-      bv[i] = bank.b[row * (size_t)(H >> 6) + (ch >> 2)];
+    for (int i = 0; i < CheckRow<RQ, XC>::NW; ++i) {
+      const int ch = lane + 64 * i < chunks ? lane + 64 * i : 0;
+      r.w[i] = load16(bank.w + row * (size_t)(H >> 2) + ch * 4);
+      r.s[i] = bank.s[row * (size_t)(H >> 6) + (ch >> 2)];
+      r.b[i] = bank.b[row * (size_t)(H >> 6) + (ch >> 2)];
+    }
+  } else {
+    const int nxc = H >> 9;
+#pragma unroll
+    for (int c = 0; c < XC; ++c) r.w[c] = load16(wrow + (lane + 64 * (c < nxc ? c : 0)) * 8);
+  }
+}
+
+template <int RQ, int XC>
+__device__ __forceinline__ float check_dot(const uint4 (&xv)[XC], const CheckRow<RQ, XC>& r,
+                                           int H, int lane) {
+  float acc = 0.0f;
+  if constexpr (RQ) {
+    const int chunks = H >> 4;
+#pragma unroll
+    for (int i = 0; i < CheckRow<RQ, XC>::NW; ++i) {
+      if (lane + 64 * i < chunks) {
+        uint4 x0 = xv[2 * i], x1 = xv[2 * i + 1];  // opaque: unpacked per row
+        asm volatile("" : "+v"(x0.x), "+v"(x0.y), "+v"(x0.z), "+v"(x0.w));
+        asm volatile("" : "+v"(x1.x), "+v"(x1.y), "+v"(x1.z), "+v"(x1.w));
+        float v[16];
+        unpack_x16(x0, x1, v);
+        acc = qgate_chunk(acc, r.w[i], v, bf16_to_f32(r.s[i]), bf16_to_f32(r.b[i]));
+      }
+    }
+  } else {
+    const int nxc = H >> 9;
+#pragma unroll
+    for (int c = 0; c < XC; ++c) {
+      if (c < nxc) {
+        // opaque copies: unpacked per row, so that the token row stays in
+        // 16 registers rather than being kept as 32 floats
+        const uint32_t xx[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+        const uint32_t ww[4] = {r.w[c].x, r.w[c].y, r.w[c].z, r.w[c].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = fmaf(bf16_lo(xx[i]), bf16_lo(ww[i]), acc);
+          acc = fmaf(bf16_hi(xx[i]), bf16_hi(ww[i]), acc);
+        }
+      }
     }
   }
-  float acc = 0.0f;
+  // every loaded register counts as used on every path, so that no load of
+  // this row is still pending where the next row's loads reuse registers
+  // (the compiler would then wait for all loads in flight)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (lane + 64 * i < chunks) {
-      float v[16];
-      unpack_x16(xv[2 * i], xv[2 * i + 1], v);
-      acc = qgate_chunk(acc, wv[i], v, bf16_to_f32(sv[i]), bf16_to_f32(bv[i]));
-    }
+  for (int i = 0; i < CheckRow<RQ, XC>::NW; ++i) {
+    asm volatile("" ::"v"(r.w[i].x), "v"(r.w[i].y), "v"(r.w[i].z), "v"(r.w[i].w));
+    if constexpr (RQ) asm volatile("" ::"v"(r.s[i]), "v"(r.b[i]));
   }
   return wave_sum(acc);
 }
 
-// One wave per token (E <= 256, H a multiple of 512 up to 4096).  RQ: the
+// One wave per token (E <= 256, H a multiple of 512 up to 512 XC).  RQ: the
 // gates are 8-bit banks (the logits came from their split planes).
-template <int RQ>
-__global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
-                                                            const float* wnorm) {
+//
+// The re-checks form one list per wave in LDS: the shared gate's row first
+// (its loads go out with the token row's, before the threshold is known),
+// then every expert within the margin; the rows stream two deep (the next
+// row's loads in flight while this one is dotted), where one row at a time
+// waited for a memory round trip per row.  At 8192 tokens the kernel is
+// bound by VALU issue (about 2000 instructions per wave, 9 re-checked rows
+// per token): the token row stays unpacked as floats, which costs
+// occupancy (5 waves per SIMD) but 32 fewer instructions per row
+// (8192 tokens 32.4 -> 27.8 us, 512 tokens 13.3 -> 11.2).
+template <int RQ, int XC>
+__global__ __launch_bounds__(256) 
+void router_select_kernel(const DecodeArgs p, const float* wnorm) {
   constexpr int P = 4;
-  constexpr int XC = 8;
+  __shared__ int s_list[4][P * 64 + 1];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wave;
   if (t >= p.T) return;
+  const int H = p.H;
   const float* lg = p.logits + (size_t)t * (p.E + 1);
-  const int nxc = p.H / 512;
-  const uint16_t* xt = p.x + (size_t)t * p.H;
-  // bf16 contract: 16-byte piece c is chunk lane + 64 c (8 values); quantized
-  // contract: pieces 2 i, 2 i + 1 are chunk lane + 64 i (16 values)
+  const uint16_t* xt = p.x + (size_t)t * H;
+  // code of a listed row: an expert, or E for the shared gate
+  auto row_ptr = [&](int code) {
+    return code < p.E ? p.router_w + (size_t)code * H : p.sgate_w;
+  };
+  auto row_bank = [&](int code) -> const QW& { return code < p.E ? p.rq : p.sgq; };
+  auto row_index = [&](int code) { return code < p.E ? (size_t)code : (size_t)0; };
+  CheckRow<RQ, XC> ra, rb;
   uint4 xv[XC];
   float nx2 = 0.0f;
 #pragma unroll
   for (int c = 0; c < XC; ++c) {
-    xv[c] = make_uint4(0, 0, 0, 0);
     if constexpr (RQ) {
       const int ch = lane + 64 * (c >> 1);
-      if (ch < (p.H >> 4)) xv[c] = load16(xt + ch * 16 + (c & 1) * 8);
+      xv[c] = load16(xt + (ch < (H >> 4) ? ch : 0) * 16 + (c & 1) * 8);
     } else {
-      if (c < nxc) xv[c] = load16(xt + (lane + 64 * c) * 8);
+      xv[c] = load16(xt + (lane + 64 * (c < (H >> 9) ? c : 0)) * 8);
     }
+  }
+  if (p.has_sg) check_load<RQ, XC>(ra, row_ptr(p.E), row_bank(p.E), 0, H, lane);
+  // logits and row bounds: unconditional loads (lanes past E read expert
+  // E - 1), so that all of them are in flight together
+  float lraw[P], wraw[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int e = min(lane + 64 * i, p.E - 1);
+    lraw[i] = lg[e];
+    wraw[i] = wnorm[e];
+  }
+  issue_fence();  // keeps these loads from being sunk into per-lane branches
+  float lv[P], wn = 0.0f, amax = 0.0f;
+  uint32_t key[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const bool on = lane + 64 * i < p.E;
+    lv[i] = on ? lraw[i] : 0.0f;
+    key[i] = on ? f32_order_key(lraw[i]) : 0u;
+    wn = fmaxf(wn, on ? wraw[i] : 0.0f);
+    amax = fmaxf(amax, fabsf(lv[i]));
+  }
+  // pieces past the row's end were loaded as the first piece: zero them
+#pragma unroll
+  for (int c = 0; c < XC; ++c) {
+    const bool live = RQ ? lane + 64 * (c >> 1) < (H >> 4) : c < (H >> 9);
+    if (!live) xv[c] = make_uint4(0, 0, 0, 0);
     const uint32_t vv[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -813,29 +877,15 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
     }
   }
   const float nx = sqrtf(wave_sum(nx2)) * (1.0f + 1.0f / 1024.0f);
-  float lv[P], wn = 0.0f, amax = 0.0f;
-  uint32_t key[P];
-#pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const int e = lane + 64 * i;
-    lv[i] = 0.0f;
-    key[i] = 0;
-    if (e < p.E) {
-      lv[i] = lg[e];
-      key[i] = f32_order_key(lv[i]);
-      wn = fmaxf(wn, wnorm[e]);
-      amax = fmaxf(amax, fabsf(lv[i]));
-    }
-  }
   wn = __uint_as_float(wave_max_u32(__float_as_uint(wn)));      // non-negative
   amax = __uint_as_float(wave_max_u32(__float_as_uint(amax)));
   // k-th largest L (with multiplicity)
   const uint32_t thr = wave_kth_largest<P>(key, p.K);
   const float tk = f32_from_order_key(thr);
   const float gam =
-      RQ ? (float)(2 * p.H - 1) * 0x1p-23f * (1.0f + 0x1p-7f) + 0x1p-17f +
-               (float)(15 + 2 * ((p.H + 1023) / 1024) + 8) * 0x1p-24f
-         : (float)(p.H - 1) * 0x1p-23f + (float)(p.H / 64 + 8) * 0x1p-24f;
+      RQ ? (float)(2 * H - 1) * 0x1p-23f * (1.0f + 0x1p-7f) + 0x1p-17f +
+               (float)(15 + 2 * ((H + 1023) / 1024) + 8) * 0x1p-24f
+         : (float)(H - 1) * 0x1p-23f + (float)(H / 64 + 8) * 0x1p-24f;
   const float delta = gam * nx * wn + 0x1p-100f * (1.0f + nx + wn);
   const float mag = amax + 2.0f * delta + 1.0f;
   const int ex = (int)((__float_as_uint(mag) >> 23) & 0xFFu);
@@ -845,21 +895,45 @@ __global__ __launch_bounds__(256) void router_select_kernel(const DecodeArgs p,
   float out[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) out[i] = lane + 64 * i < p.E ? round_bf16(lv[i]) : 0.0f;
+  // the list: the shared gate, then the experts within the margin in index order
+  int* list = s_list[wave];
+  int n = p.has_sg ? 1 : 0;
+  if (p.has_sg && lane == 0) list[0] = p.E;
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    uint64_t m = __ballot(lane + 64 * i < p.E && lv[i] >= lo);
-    while (m) {
-      const int bit = __ffsll((unsigned long long)m) - 1;
-      m &= m - 1;
-      const int e = bit + 64 * i;
-      const float c = RQ ? q8_contract_dot(xv, p.rq, (size_t)e, p.H)
-                         : contract_dot<XC>(xv, nxc, p.router_w + (size_t)e * p.H);
-      if (lane == bit) out[i] = round_bf16(c);
-    }
+    const bool in = lane + 64 * i < p.E && lv[i] >= lo;
+    const uint64_t m = __ballot(in);
+    if (in) list[n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
+        lane + 64 * i;
+    n += __popcll(m);
   }
+  __builtin_amdgcn_wave_barrier();
   float sg_logit = 0.0f;
-  if (p.has_sg)
-    sg_logit = RQ ? q8_contract_dot(xv, p.sgq, 0, p.H) : contract_dot<XC>(xv, nxc, p.sgate_w);
+  auto record = [&](int code, float c) {
+    if (code >= p.E) {
+      sg_logit = c;
+    } else {
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if ((code >> 6) == i && lane == (code & 63)) out[i] = round_bf16(c);
+    }
+  };
+  int ca = p.E;
+  if (!p.has_sg && n > 0) {  // n = 0 only for NaN logits
+    ca = __builtin_amdgcn_readfirstlane(list[0]);
+    check_load<RQ, XC>(ra, row_ptr(ca), row_bank(ca), row_index(ca), H, lane);
+  }
+  for (int j = 0; j < n; j += 2) {
+    const int cb = __builtin_amdgcn_readfirstlane(list[min(j + 1, n - 1)]);
+    check_load<RQ, XC>(rb, row_ptr(cb), row_bank(cb), row_index(cb), H, lane);
+    record(ca, check_dot<RQ, XC>(xv, ra, H, lane));
+    if (j + 1 >= n) break;
+    const int cn = __builtin_amdgcn_readfirstlane(list[min(j + 2, n - 1)]);
+    check_load<RQ, XC>(ra, row_ptr(cn), row_bank(cn), row_index(cn), H, lane);
+    record(cb, check_dot<RQ, XC>(xv, rb, H, lane));
+    ca = cn;
+  }
   finish_route<P>(p, t, out, sg_logit);
 }
 
@@ -1463,13 +1537,21 @@ hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split
     lo.router_w = split + (size_t)a.E * a.H;
     launch_logits<false, false>(hi, nullptr, s);
     launch_logits<true, false>(lo, nullptr, s);
-    hipLaunchKernelGGL(router_select_kernel<1>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                       (const float*)wnorm);
+    if (a.H <= 2048)
+      hipLaunchKernelGGL((router_select_kernel<1, 4>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                         (const float*)wnorm);
+    else
+      hipLaunchKernelGGL((router_select_kernel<1, 8>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                         (const float*)wnorm);
   } else {
     // the row norms come from the first token tile's workgroups
     launch_logits<false, true>(a, wnorm, s);
-    hipLaunchKernelGGL(router_select_kernel<0>, dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                       (const float*)wnorm);
+    if (a.H <= 2048)
+      hipLaunchKernelGGL((router_select_kernel<0, 4>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                         (const float*)wnorm);
+    else
+      hipLaunchKernelGGL((router_select_kernel<0, 8>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
+                         (const float*)wnorm);
   }
   RMOE_CHECK_LAUNCH();
   return hipSuccess;
