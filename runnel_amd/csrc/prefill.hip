@@ -202,7 +202,14 @@ __global__ __launch_bounds__(kSortThreads) void prefill_hist_kernel(const Prefil
   __syncthreads();
   int r0, r1;
   sort_slice(p.T * p.K, gridDim.x, blockIdx.x, r0, r1);
-  for (int r = r0 + tid; r < r1; r += kSortThreads) atomicAdd(&s_hist[bucket_of(p, r)], 1);
+  // two rows per thread per step, both loads issued before either is used
+  for (int r = r0 + tid; r < r1; r += 2 * kSortThreads) {
+    const int ra = r, rb = r + kSortThreads;
+    const int ea = bucket_of(p, ra), eb = bucket_of(p, min(rb, r1 - 1));
+    issue_fence();
+    atomicAdd(&s_hist[ea], 1);
+    if (rb < r1) atomicAdd(&s_hist[eb], 1);
+  }
   __syncthreads();
   for (int b = tid; b < NB; b += kSortThreads) p.hist[blockIdx.x * NB + b] = s_hist[b];
 }
@@ -215,59 +222,84 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   const int NW = gridDim.x;
   const int w = blockIdx.x;
   __shared__ int s_hist[kSortWaves * (kPrefillMaxExperts + 2)];
-  __shared__ int s_scan[2][kSortThreads];
+  __shared__ int s_wsum[2][kSortWaves];
   __shared__ int s_shared_off;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   for (int i = tid; i < kSortWaves * NB; i += kSortThreads) s_hist[i] = 0;
 
-  // Per bucket: total rows, rows in earlier slices, m-tiles.
-  int rows_b = 0, before_b = 0, tiles_b = 0;
-  if (tid < NB) {
-    if (tid == p.E) {
-      rows_b = p.has_shared ? p.T : 0;
-    } else {
-      for (int v = 0; v < NW; ++v) {
-        const int c = p.hist[v * NB + tid];
-        rows_b += c;
-        before_b += v < w ? c : 0;
-      }
-    }
-    tiles_b = (rows_b + p.bm - 1) / p.bm;
-  }
-  s_scan[0][tid] = rows_b;
-  s_scan[1][tid] = tiles_b;
-  __syncthreads();
-  for (int d = 1; d < kSortThreads; d <<= 1) {
-    const int a = tid >= d ? s_scan[0][tid - d] : 0;
-    const int b = tid >= d ? s_scan[1][tid - d] : 0;
-    __syncthreads();
-    s_scan[0][tid] += a;
-    s_scan[1][tid] += b;
-    __syncthreads();
-  }
-
-  // this workgroup's slice, one run per wave: per-wave counts
+  // this workgroup's slice, one run per wave
   const int n = p.T * p.K;
   int r0, r1;
   sort_slice(n, NW, w, r0, r1);
   const int per = ((r1 - r0 + kSortWaves - 1) / kSortWaves + 63) & ~63;
   const int q0 = min(r1, r0 + wave * per);
   const int q1 = min(r1, q0 + per);
+
+  // Per bucket: total rows, rows in earlier slices, m-tiles.  The slices'
+  // counts are loaded 16 at a time (a loop of single loads waited for each).
+  int rows_b = 0, before_b = 0, tiles_b = 0;
+  if (tid < NB) {
+    if (tid == p.E) {
+      rows_b = p.has_shared ? p.T : 0;
+    } else {
+      for (int v0 = 0; v0 < NW; v0 += 16) {
+        int c[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) c[u] = p.hist[min(v0 + u, NW - 1) * NB + tid];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int v = v0 + u;
+          rows_b += v < NW ? c[u] : 0;
+          before_b += v < w ? c[u] : 0;
+        }
+      }
+    }
+    tiles_b = (rows_b + p.bm - 1) / p.bm;
+  }
+  // inclusive scans of rows_b and tiles_b over the buckets: within each
+  // wave, then the earlier waves' totals added
+  int sr = rows_b, st = tiles_b;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int a = __shfl_up(sr, d, 64);
+    const int b = __shfl_up(st, d, 64);
+    if (lane >= d) {
+      sr += a;
+      st += b;
+    }
+  }
+  if (lane == 63) {
+    s_wsum[0][wave] = sr;
+    s_wsum[1][wave] = st;
+  }
+
+  // per-wave counts of this wave's run (two chunks of 64 rows per step)
   int* my = s_hist + wave * NB;
-  for (int r = q0 + lane; r < q1; r += 64) atomicAdd(&my[bucket_of(p, r)], 1);
+  __syncthreads();  // the zeroed counts and the wave totals
+  for (int c0 = q0; c0 < q1; c0 += 128) {
+    const int ra = c0 + lane, rb = c0 + 64 + lane;
+    const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
+    issue_fence();
+    if (ra < q1) atomicAdd(&my[ea], 1);
+    if (rb < q1) atomicAdd(&my[eb], 1);
+  }
+  for (int v = 0; v < wave; ++v) {
+    sr += s_wsum[0][v];
+    st += s_wsum[1][v];
+  }
   __syncthreads();
 
   if (tid < NB) {
-    const int row_off = s_scan[0][tid] - rows_b;
-    const int t0 = s_scan[1][tid] - tiles_b;
+    const int row_off = sr - rows_b;
+    const int t0 = st - tiles_b;
     if (w == 0) {
       p.offs[tid] = row_off;
       p.tile_offs[tid] = t0;
       if (tid == NB - 1) {
-        p.offs[NB] = s_scan[0][tid];
-        p.tile_offs[NB] = s_scan[1][tid];
+        p.offs[NB] = sr;
+        p.tile_offs[NB] = st;
       }
       for (int i = 0; i < tiles_b; ++i) {
         const int r = row_off + i * p.bm;
@@ -294,10 +326,7 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
 
   // Stable ranking: each wave walks its run in order, 64 at a time; the
   // lanes holding one bucket find each other with one ballot per id bit.
-  for (int c0 = q0; c0 < q1; c0 += 64) {
-    const int r = c0 + lane;
-    const bool v = r < q1;
-    const int e = v ? bucket_of(p, r) : 0;
+  auto rank_chunk = [&](int r, int e, bool v) {
     uint64_t mask = __ballot(v);
 #pragma unroll
     for (int b = 0; b < 10; ++b) {
@@ -314,6 +343,13 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
     __builtin_amdgcn_wave_barrier();
     if (v && (mask >> lane) == 1ull) my[e] += __popcll(mask);
     __builtin_amdgcn_wave_barrier();
+  };
+  for (int c0 = q0; c0 < q1; c0 += 128) {
+    const int ra = c0 + lane, rb = c0 + 64 + lane;
+    const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
+    issue_fence();
+    rank_chunk(ra, ra < q1 ? ea : 0, ra < q1);
+    if (c0 + 64 < q1) rank_chunk(rb, rb < q1 ? eb : 0, rb < q1);
   }
 }
 
