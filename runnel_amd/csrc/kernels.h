@@ -150,7 +150,7 @@ struct PrefillArgs {
   QW gu, dn, sgu, sdn;
   int32_t* rows;           // [T K + T] source row of each sorted row
   int32_t* offs;           // [E + 3] rows per bucket (E: shared, E + 1: bad ids)
-  int32_t* tile_offs;      // [E + 3] m-tiles per bucket; [E + 2] = total
+  int32_t* tile_offs;      // [E + 3]: [E + 1] = full m-tiles, [E + 2] = all m-tiles
   int32_t* tile_desc;      // [m-tiles][4]: bucket, first sorted row, rows, 0
   int32_t* hist;           // [sort slices][E + 2] rows per bucket of each slice
   uint16_t* act;           // [T K + T, I] bf16, sorted order

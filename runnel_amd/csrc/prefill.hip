@@ -146,25 +146,43 @@ struct Tile {
 // Items are (m-tile, n-tile) with n innermost, cut into 8 contiguous runs,
 // one per XCD (workgroup i runs on XCD i % 8): the n-tiles of one m-tile
 // share its A rows in that XCD's L2, and the m-tiles of one expert share
-// its weight columns there.
+// its weight columns there.  For 128-row tiles the sort lists the full
+// m-tiles first and the partial ones (each bucket's last) after them, and
+// each XCD takes its run of full items before its run of partial ones: the
+// cheap partial tiles fill the last round instead of a full tile starting
+// late (8192 tokens: down 255.9 -> 246.6 us).
 __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& t) {
-  const int MT = p.dense ? (p.T + p.bm - 1) / p.bm : p.tile_offs[p.E + 2];
-  const int total = nt * MT;
-  const int L = (total + 7) >> 3;
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
-  if (slot >= L) return false;
-  const int item = xcd * L + slot;
-  if (item >= total) return false;
-  const int m = item / nt;
-  t.n = item - m * nt;
   if (p.dense) {
+    const int MT = (p.T + p.bm - 1) / p.bm;
+    const int total = nt * MT;
+    const int L = (total + 7) >> 3;
+    if (slot >= L) return false;
+    const int item = xcd * L + slot;
+    if (item >= total) return false;
+    const int m = item / nt;
+    t.n = item - m * nt;
     // rows m bm .. of the one bank, in order
     t.bucket = 0;
     t.row0 = m * p.bm;
     t.nrows = min(p.bm, p.T - t.row0);
     return true;
   }
+  const int nf = nt * p.tile_offs[p.E + 1];  // full items
+  const int np = nt * p.tile_offs[p.E + 2] - nf;
+  const int lf = (nf + 7) >> 3, lp = (np + 7) >> 3;
+  int item;
+  if (slot < lf) {
+    item = xcd * lf + slot;
+    if (item >= nf) return false;
+  } else {
+    const int i = xcd * lp + (slot - lf);
+    if (slot - lf >= lp || i >= np) return false;
+    item = nf + i;
+  }
+  const int m = item / nt;
+  t.n = item - m * nt;
   const int4 d = reinterpret_cast<const int4*>(p.tile_desc)[m];
   t.bucket = d.x;
   t.row0 = d.y;
@@ -222,8 +240,9 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   const int NW = gridDim.x;
   const int w = blockIdx.x;
   __shared__ int s_hist[kSortWaves * (kPrefillMaxExperts + 2)];
-  __shared__ int s_wsum[2][kSortWaves];
+  __shared__ int s_wsum[3][kSortWaves];
   __shared__ int s_shared_off;
+  __shared__ int s_full;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -237,9 +256,10 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   const int q0 = min(r1, r0 + wave * per);
   const int q1 = min(r1, q0 + per);
 
-  // Per bucket: total rows, rows in earlier slices, m-tiles.  The slices'
-  // counts are loaded 16 at a time (a loop of single loads waited for each).
-  int rows_b = 0, before_b = 0, tiles_b = 0;
+  // Per bucket: total rows, rows in earlier slices, full m-tiles and the
+  // partial one.  The slices' counts are loaded 16 at a time (a loop of
+  // single loads waited for each).
+  int rows_b = 0, before_b = 0, full_b = 0, part_b = 0;
   if (tid < NB) {
     if (tid == p.E) {
       rows_b = p.has_shared ? p.T : 0;
@@ -256,23 +276,31 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
         }
       }
     }
-    tiles_b = (rows_b + p.bm - 1) / p.bm;
+    // 32-row tiles (short prefill, weight-stream bound) keep bucket order:
+    // every m-tile counts as full (512 tokens: 254 against 248 us with the
+    // partial tiles listed last)
+    const bool split = p.bm == kPrefillBM;
+    full_b = split ? rows_b / p.bm : (rows_b + p.bm - 1) / p.bm;
+    part_b = split && rows_b - full_b * p.bm > 0 ? 1 : 0;
   }
-  // inclusive scans of rows_b and tiles_b over the buckets: within each
-  // wave, then the earlier waves' totals added
-  int sr = rows_b, st = tiles_b;
+  // inclusive scans of rows_b, full_b and part_b over the buckets: within
+  // each wave, then the earlier waves' totals added
+  int sr = rows_b, sf = full_b, sp = part_b;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int a = __shfl_up(sr, d, 64);
-    const int b = __shfl_up(st, d, 64);
+    const int b = __shfl_up(sf, d, 64);
+    const int c = __shfl_up(sp, d, 64);
     if (lane >= d) {
       sr += a;
-      st += b;
+      sf += b;
+      sp += c;
     }
   }
   if (lane == 63) {
     s_wsum[0][wave] = sr;
-    s_wsum[1][wave] = st;
+    s_wsum[1][wave] = sf;
+    s_wsum[2][wave] = sp;
   }
 
   // per-wave counts of this wave's run (two chunks of 64 rows per step)
@@ -287,25 +315,29 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   }
   for (int v = 0; v < wave; ++v) {
     sr += s_wsum[0][v];
-    st += s_wsum[1][v];
+    sf += s_wsum[1][v];
+    sp += s_wsum[2][v];
   }
+  if (tid == NB - 1) s_full = sf;
   __syncthreads();
 
   if (tid < NB) {
     const int row_off = sr - rows_b;
-    const int t0 = st - tiles_b;
     if (w == 0) {
+      // the full m-tiles in bucket order, then the partial ones
       p.offs[tid] = row_off;
-      p.tile_offs[tid] = t0;
       if (tid == NB - 1) {
         p.offs[NB] = sr;
-        p.tile_offs[NB] = st;
+        p.tile_offs[NB - 1] = sf;  // full m-tiles
+        p.tile_offs[NB] = sf + sp;
       }
-      for (int i = 0; i < tiles_b; ++i) {
-        const int r = row_off + i * p.bm;
-        *reinterpret_cast<int4*>(p.tile_desc + 4 * (t0 + i)) =
-            make_int4(tid, r, min(p.bm, row_off + rows_b - r), 0);
-      }
+      const int f0 = sf - full_b;
+      for (int i = 0; i < full_b; ++i)
+        *reinterpret_cast<int4*>(p.tile_desc + 4 * (f0 + i)) =
+            make_int4(tid, row_off + i * p.bm, min(p.bm, rows_b - i * p.bm), 0);
+      if (part_b)
+        *reinterpret_cast<int4*>(p.tile_desc + 4 * (s_full + sp - 1)) =
+            make_int4(tid, row_off + full_b * p.bm, rows_b - full_b * p.bm, 0);
     }
     // per-wave bases of this bucket in this slice
     int base = row_off + before_b;
@@ -1185,8 +1217,10 @@ template <int BITS, int BM>
 void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
   const int nt_gu = a.I / Engine<BITS, BM, 0>::TN;
   const int nt_dn = a.H / Engine<BITS, BM, 1>::TN;
-  const int g_gu = 8 * ((nt_gu * mt + 7) / 8);
-  const int g_dn = 8 * ((nt_dn * mt + 7) / 8);
+  // the full and the partial items are split over the XCDs separately: up
+  // to one more slot per XCD for each
+  const int g_gu = 8 * ((nt_gu * mt + 7) / 8 + 2);
+  const int g_dn = 8 * ((nt_dn * mt + 7) / 8 + 2);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu),
                      dim3(Engine<BITS, BM, 0>::THREADS), 0, s, a, nt_gu);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn),
