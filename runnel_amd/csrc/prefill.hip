@@ -150,7 +150,9 @@ struct Tile {
 // m-tiles first and the partial ones (each bucket's last) after them, and
 // each XCD takes its run of full items before its run of partial ones: the
 // cheap partial tiles fill the last round instead of a full tile starting
-// late (8192 tokens: down 255.9 -> 246.6 us).
+// late (8192 tokens: down 255.9 -> 246.6 us).  The partial m-tiles are
+// dealt to the XCDs in turn, largest first, so each XCD ends on its
+// smallest ones.
 __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& t) {
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
@@ -169,20 +171,25 @@ __device__ __forceinline__ bool decode_tile(const PrefillArgs& p, int nt, Tile& 
     t.nrows = min(p.bm, p.T - t.row0);
     return true;
   }
-  const int nf = nt * p.tile_offs[p.E + 1];  // full items
-  const int np = nt * p.tile_offs[p.E + 2] - nf;
-  const int lf = (nf + 7) >> 3, lp = (np + 7) >> 3;
-  int item;
+  const int mf = p.tile_offs[p.E + 1];  // full m-tiles
+  const int mp = p.tile_offs[p.E + 2] - mf;
+  const int nf = nt * mf;
+  const int lf = (nf + 7) >> 3;
+  int m;
   if (slot < lf) {
-    item = xcd * lf + slot;
+    const int item = xcd * lf + slot;
     if (item >= nf) return false;
+    m = item / nt;
+    t.n = item - m * nt;
   } else {
-    const int i = xcd * lp + (slot - lf);
-    if (slot - lf >= lp || i >= np) return false;
-    item = nf + i;
+    // partial m-tiles (largest first) dealt to the XCDs in turn, the
+    // n-tiles of one m-tile together
+    const int s2 = slot - lf;
+    const int j = s2 / nt;
+    if (xcd + 8 * j >= mp) return false;
+    m = mf + xcd + 8 * j;
+    t.n = s2 - j * nt;
   }
-  const int m = item / nt;
-  t.n = item - m * nt;
   const int4 d = reinterpret_cast<const int4*>(p.tile_desc)[m];
   t.bucket = d.x;
   t.row0 = d.y;
@@ -243,6 +250,7 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   __shared__ int s_wsum[3][kSortWaves];
   __shared__ int s_shared_off;
   __shared__ int s_full;
+  __shared__ int s_cls[8];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -335,9 +343,6 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
       for (int i = 0; i < full_b; ++i)
         *reinterpret_cast<int4*>(p.tile_desc + 4 * (f0 + i)) =
             make_int4(tid, row_off + i * p.bm, min(p.bm, rows_b - i * p.bm), 0);
-      if (part_b)
-        *reinterpret_cast<int4*>(p.tile_desc + 4 * (s_full + sp - 1)) =
-            make_int4(tid, row_off + full_b * p.bm, rows_b - full_b * p.bm, 0);
     }
     // per-wave bases of this bucket in this slice
     int base = row_off + before_b;
@@ -352,6 +357,30 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
     }
   }
   __syncthreads();
+  if (w == 0 && p.bm == kPrefillBM) {
+    // the partial m-tiles after the full ones, largest first (counting sort
+    // by 16-row blocks; the order within a class does not matter)
+    if (tid < 8) s_cls[tid] = 0;
+    __syncthreads();
+    const int rem = rows_b - full_b * p.bm;
+    const int cls = 8 - ((rem + 15) >> 4);  // 0: eight blocks
+    if (part_b) atomicAdd(&s_cls[cls], 1);
+    __syncthreads();
+    if (tid == 0) {
+      int a = 0;
+      for (int c = 0; c < 8; ++c) {
+        const int k = s_cls[c];
+        s_cls[c] = a;
+        a += k;
+      }
+    }
+    __syncthreads();
+    if (part_b) {
+      const int pos = atomicAdd(&s_cls[cls], 1);
+      *reinterpret_cast<int4*>(p.tile_desc + 4 * (s_full + pos)) =
+          make_int4(tid, sr - rows_b + full_b * p.bm, rem, 0);
+    }
+  }
   if (p.has_shared)
     for (int t = w * kSortThreads + tid; t < p.T; t += NW * kSortThreads)
       p.rows[s_shared_off + t] = n + t;
@@ -1217,10 +1246,10 @@ template <int BITS, int BM>
 void launch_gemms(const PrefillArgs& a, int mt, hipStream_t s) {
   const int nt_gu = a.I / Engine<BITS, BM, 0>::TN;
   const int nt_dn = a.H / Engine<BITS, BM, 1>::TN;
-  // the full and the partial items are split over the XCDs separately: up
-  // to one more slot per XCD for each
-  const int g_gu = 8 * ((nt_gu * mt + 7) / 8 + 2);
-  const int g_dn = 8 * ((nt_dn * mt + 7) / 8 + 2);
+  // the full items are split over the XCDs in runs, the partial m-tiles
+  // dealt in turn: up to 1 + nt more slots per XCD than an even split
+  const int g_gu = 8 * ((nt_gu * mt + 7) / 8 + 1 + nt_gu);
+  const int g_dn = 8 * ((nt_dn * mt + 7) / 8 + 1 + nt_dn);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 0>), dim3(g_gu),
                      dim3(Engine<BITS, BM, 0>::THREADS), 0, s, a, nt_gu);
   hipLaunchKernelGGL((prefill_gemm_kernel<BITS, BM, 1>), dim3(g_dn),
