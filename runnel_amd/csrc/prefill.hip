@@ -57,6 +57,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kSortRowsPerSlice = 2048;  // rows per sorting workgroup
+// up to this many rows one workgroup sorts them all, without the
+// histogram pass (a launch of ~4.6 us)
+constexpr int kSortOneSliceRows = 8192;
 constexpr int kPad = 8;                         // bf16 of padding per LDS row
 
 // K advances in chunks of KC values.  Each lane group g = l / 16 owns KC / 4
@@ -271,7 +274,7 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
   if (tid < NB) {
     if (tid == p.E) {
       rows_b = p.has_shared ? p.T : 0;
-    } else {
+    } else if (NW > 1) {
       for (int v0 = 0; v0 < NW; v0 += 16) {
         int c[16];
 #pragma unroll
@@ -284,6 +287,23 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
         }
       }
     }
+  }
+
+  // per-wave counts of this wave's run (two chunks of 64 rows per step)
+  int* my = s_hist + wave * NB;
+  __syncthreads();  // the zeroed counts
+  for (int c0 = q0; c0 < q1; c0 += 128) {
+    const int ra = c0 + lane, rb = c0 + 64 + lane;
+    const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
+    issue_fence();
+    if (ra < q1) atomicAdd(&my[ea], 1);
+    if (rb < q1) atomicAdd(&my[eb], 1);
+  }
+  __syncthreads();  // every wave's counts
+  if (tid < NB) {
+    // one slice (no histogram pass): the totals are this workgroup's counts
+    if (NW == 1 && tid != p.E)
+      for (int v = 0; v < kSortWaves; ++v) rows_b += s_hist[v * NB + tid];
     // 32-row tiles (short prefill, weight-stream bound) keep bucket order:
     // every m-tile counts as full (512 tokens: 254 against 248 us with the
     // partial tiles listed last)
@@ -311,16 +331,7 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
     s_wsum[2][wave] = sp;
   }
 
-  // per-wave counts of this wave's run (two chunks of 64 rows per step)
-  int* my = s_hist + wave * NB;
-  __syncthreads();  // the zeroed counts and the wave totals
-  for (int c0 = q0; c0 < q1; c0 += 128) {
-    const int ra = c0 + lane, rb = c0 + 64 + lane;
-    const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
-    issue_fence();
-    if (ra < q1) atomicAdd(&my[ea], 1);
-    if (rb < q1) atomicAdd(&my[eb], 1);
-  }
+  __syncthreads();  // the wave totals
   for (int v = 0; v < wave; ++v) {
     sr += s_wsum[0][v];
     sf += s_wsum[1][v];
@@ -1234,6 +1245,7 @@ int prefill_tile_rows(int T, int K, int E) {
 
 int prefill_sort_slices(int T, int K) {
   const long n = (long)T * K;
+  if (n <= kSortOneSliceRows) return 1;
   const long nw = (n + kSortRowsPerSlice - 1) / kSortRowsPerSlice;
   return (int)(nw < 1 ? 1 : nw > kPrefillMaxSlices ? kPrefillMaxSlices : nw);
 }
@@ -1317,7 +1329,8 @@ hipError_t launch_prefill(const PrefillArgs& args, int bits, bool combine, hipSt
   a.bm = prefill_tile_rows(a.T, a.K, a.E);
   if (a.bm == kPrefillBM && !buffer_offsets_fit(a, bits)) return hipErrorInvalidValue;
   const int nw = prefill_sort_slices(a.T, a.K);
-  hipLaunchKernelGGL(prefill_hist_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
+  // one slice: the place kernel counts its rows itself
+  if (nw > 1) hipLaunchKernelGGL(prefill_hist_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
   hipLaunchKernelGGL(prefill_place_kernel, dim3(nw), dim3(kSortThreads), 0, s, a);
   const int mt = prefill_max_mtiles(a.T, a.K, a.E, a.bm);
   if (bits == 8) {
