@@ -69,6 +69,9 @@ constexpr int kMaxFusedRowsPerWave = 1;
 constexpr int kFusedMaxExperts = 256;
 constexpr int kFusedH = 2048;
 constexpr int kFusedI = 512;
+// XCD-per-unit kernel: exactly 256 workgroups (32 on each of 8 XCDs).
+constexpr int kFusedXcdGrid = 256;
+constexpr bool kFusedXcdDownEarly = true;  // routed down rows issued with gate/up
 // ---- few-token decode (decode.hip): 2..8 tokens at the shapes above.
 constexpr int kFewMaxTokens = 8;
 
@@ -91,6 +94,11 @@ struct FusedScratch {
   uint32_t logits[8][kFusedMaxExperts];   // one copy per XCD (written and read there)
   uint32_t act[kMaxFusedUnits * kFusedI];
   uint32_t xs[2][kFusedH];
+  // XCD-per-unit kernel
+  uint32_t xact[8][kFusedI];                  // routed act of XCD x (read there)
+  uint32_t sact[2][kFusedI];                  // shared act, by layer parity
+  uint32_t ys[2][kMaxFusedUnits][kFusedH];    // unit outputs, by layer parity
+  uint32_t xl[8][2][kFusedH];                 // combined layer input of XCD x
 };
 
 struct FusedArgs {

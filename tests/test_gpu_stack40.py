@@ -29,10 +29,43 @@ def torch_cuda():
     return torch
 
 
-def _contract_mismatches(got_bits, ref_bits):
+def _step(v):
+    """One bf16 step (unit in the last place) at |v|."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def _rounding_allowance(L, xin, idx, scores):
+    """Per-element error that a different (valid) fp32 evaluation order can
+    cause under the contract: one bf16 step of every rounded intermediate
+    the combine sees -- each unit output weighted by its score, each score
+    weighted by its unit output, the shared term likewise -- plus one step
+    of the block output and of the residual sum.  Near cancellation (the
+    residual and the block output of opposite sign) these steps are large
+    against the result, which a relative bound alone misses."""
+    y = M.switch_glu(L, xin, idx).astype(np.float64)[0]          # [k, H]
+    s = scores.astype(np.float64)[0][:, None]
+    allow = (np.abs(s) * _step(y) + _step(s) * np.abs(y)).sum(0)
+    block = (s * y).sum(0)
+    if L.shared_gate_up is not None:
+        ysh = M.expert_ffn(L.shared_gate_up, L.shared_down, 0,
+                           M.bf16_to_f32(xin)).astype(np.float64)[0]
+        sg = 1.0
+        if L.shared_gate_w is not None:
+            sgw = L.shared_gate_w
+            sl = M.round_bf16(M.gate_logits(xin, sgw if isinstance(sgw, M.QWeight)
+                                            else sgw[None, :])[:, 0])
+            sg = float(M.round_bf16(M._sigmoid32(sl))[0])
+        allow += abs(sg) * _step(ysh) + _step(sg) * np.abs(ysh)
+        block = block + sg * ysh
+    out = block + M.bf16_to_f32(xin).astype(np.float64)[0]
+    return allow + _step(block) + _step(out)
+
+
+def _contract_mismatches(got_bits, ref_bits, allow=0.0):
     g = M.bf16_to_f32(got_bits).astype(np.float64)
     r = M.bf16_to_f32(ref_bits).astype(np.float64)
-    tol = np.maximum(np.abs(r), 1e-3) * 2.0 ** -6 + 1e-6
+    tol = np.maximum(np.abs(r), 1e-3) * 2.0 ** -6 + 1e-6 + allow
     return int((np.abs(g - r) > tol).sum())
 
 
@@ -63,7 +96,7 @@ def test_forty_layer_chain_matches_the_oracle_at_every_layer(torch_cuda):
     for l in range(N_LAYERS):
         L = layer_from_dev(stack[l])
         xin = host_bf16(ys[l])
-        ref, ref_idx, _ = M.block_forward(L, xin, residual_bits=xin)
+        ref, ref_idx, ref_scores = M.block_forward(L, xin, residual_bits=xin)
         one, idx, _ = native.moe_block(hs[l], ys[l], residual=ys[l], return_routing=True,
                                        workspace=ws, check=False)
         torch.cuda.synchronize()
@@ -71,7 +104,12 @@ def test_forty_layer_chain_matches_the_oracle_at_every_layer(torch_cuda):
         assert torch.equal(one, ys[l + 1]), f"layer {l}"
         assert np.array_equal(idx.cpu().numpy(), ref_idx), f"layer {l}"
         got = host_bf16(ys[l + 1])
-        assert _contract_mismatches(got, ref) <= 4, f"layer {l}"
+        # every element within 2^-6 of the contract plus the steps of its
+        # rounded intermediates (a different fp32 order flips a rounding
+        # point now and then; near cancellation that is several steps of
+        # the result)
+        allow = _rounding_allowance(L, xin, ref_idx, ref_scores)
+        assert _contract_mismatches(got, ref, allow) == 0, f"layer {l}"
         if split_at is None:
             nxt, own_idx, _ = M.block_forward(L, cur_ref, residual_bits=cur_ref)
             if not np.array_equal(np.sort(own_idx, -1), np.sort(ref_idx, -1)):
