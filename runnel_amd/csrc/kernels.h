@@ -71,7 +71,7 @@ constexpr int kFusedH = 2048;
 constexpr int kFusedI = 512;
 // XCD-per-unit kernel: exactly 256 workgroups (32 on each of 8 XCDs).
 constexpr int kFusedXcdGrid = 256;
-constexpr bool kFusedXcdDownEarly = true;  // routed down rows issued with gate/up
+constexpr bool kFusedXcdDownEarly = false;  // routed down rows issued after the gate/up math
 // ---- few-token decode (decode.hip): 2..8 tokens at the shapes above.
 constexpr int kFewMaxTokens = 8;
 
