@@ -212,7 +212,8 @@ int rmoe_gather_qmm(const uint16_t* x, int32_t x_rows,
  * residual != NULL, out[t] = bf16(residual[t] + out[t]).  indices_out /
  * scores_out may be NULL.  x, residual, out bf16 [tokens, hidden]; out may
  * alias residual but not x.  One token of a layer with hidden 2048, inter
- * 512, top_k <= 8 and experts <= 256 runs as one single-launch kernel (see
+ * 512, top_k <= 8 and experts <= 256 runs as one single-launch kernel on a
+ * device of at least 256 CUs in 8 XCDs, such as MI355X (see
  * rmoe_workspace_status_offset); other calls that route fewer than 64
  * (token, slot) rows take the router, gate/up and down kernels; calls that
  * route 64 or more take the expert-sorted path, which needs out and
@@ -250,8 +251,9 @@ int rmoe_moe_block_noalloc(const rmoe_layer* layer, const uint16_t* x, int32_t t
  * rmoe_chain_table_pack into rmoe_chain_table_bytes(n) bytes, copied by the
  * caller to device memory, and passed as device_table; layer0 describes the
  * common shape.  Needs hidden 2048, inter 512, top_k <= 8 (plus an optional
- * shared expert) and experts <= 256; rmoe_chain_table_pack checks the
- * shape without touching the device.  x, out bf16 [hidden]. */
+ * shared expert), experts <= 256 and a device of at least 256 CUs in 8 XCDs
+ * (RMOE_EINVAL otherwise); rmoe_chain_table_pack checks the shape without
+ * touching the device.  x, out bf16 [hidden]. */
 size_t rmoe_chain_table_bytes(int32_t n_layers);
 int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers,
                           void* host_table);

@@ -348,23 +348,15 @@ bool fused_shape_ok(const rmoe_layer* L) {
          L->top_k <= rmoe::kMaxFusedRouted && L->experts <= rmoe::kFusedMaxExperts;
 }
 
-// The single-launch decode kernel also needs one resident workgroup per CU
-// with enough waves to give every down row its own wave.
+// The single-launch decode kernel also needs its grid: one resident
+// workgroup on each of 256 CUs, 32 on each of the 8 XCDs.
 bool fused_eligible(const rmoe_layer* L, int* grid) {
   if (!fused_shape_ok(L)) return false;
-  const int units = L->top_k + (L->shared_gate_up.w ? 1 : 0);
   int g = 0;
   if (rmoe::fused_grid(L->gate_up.bits, router_quantized(L), L->post_norm_w != nullptr, &g) !=
       hipSuccess)
     return false;
-  const int waves = g * (rmoe::kFusedThreads / 64);
-  // the router rows are computed once per XCD by its g / 8 workgroups
-  if (g % 8 != 0 || g < L->experts) return false;
-  if (waves < rmoe::kFusedH * 1 / rmoe::kMaxFusedRowsPerWave) return false;
-  if ((units * rmoe::kFusedI + waves - 1) / waves > rmoe::kMaxFusedPairsPerWave) return false;
-  // every workgroup must own at least one gate/up pair (the epoch hand-over
-  // relies on workgroup 0 consuming a value from each of them)
-  if (units * rmoe::kFusedI < waves) return false;
+  if (g != rmoe::kFusedXcdGrid) return false;
   *grid = g;
   return true;
 }
@@ -902,7 +894,8 @@ int rmoe_chain_table_pack(const rmoe_layer* layers, int32_t n_layers, void* host
                 rmoe::kFusedH, rmoe::kFusedI, rmoe::kMaxFusedRouted, rmoe::kFusedMaxExperts,
                 layers[0].hidden, layers[0].inter, layers[0].top_k, layers[0].experts);
   if (!fused_eligible(&layers[0], &grid))
-    return fail(RMOE_EINVAL, "chained decode needs one resident workgroup per CU");
+    return fail(RMOE_EINVAL, "chained decode needs a device of at least %d CUs in 8 XCDs",
+                rmoe::kFusedXcdGrid);
   for (int i = 0; i < n_layers; ++i)
     static_cast<rmoe::FusedLayer*>(host_table)[i] = fused_layer(&layers[i]);
   return ok();

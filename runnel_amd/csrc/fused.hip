@@ -1,39 +1,47 @@
 // Single-launch batch-1 decode of one or more MoE layers (gfx950).
 //
-// One workgroup of 8 waves per CU, launched cooperatively so every
+// 256 workgroups of 8 waves, one per CU and 32 on each of the 8 XCDs
+// (workgroup i runs on XCD i % 8), launched cooperatively so that every
 // workgroup is resident (inside a captured graph: a plain launch of the same
-// grid, see launch_fused_decode).  Per layer:
+// grid, see launch_fused_decode).  Routed slot u (u < K <= 8) is computed
+// whole by XCD u: its gate/up pairs, the SwiGLU activations (handed over
+// inside that XCD's L2) and all of its down rows, one bf16 output word per
+// row.  The shared expert does not depend on the routing: XCD x computes its
+// pairs 64 x .. 64 x + 63 right after the router rows (handed over
+// device-wide, off the routed critical path) and its down rows
+// 256 x .. 256 x + 255.  A layer therefore has one device-wide hand-over on
+// its critical path: every XCD combines the unit outputs of its own 2048
+// rows (each workgroup 64 rows), and the combined layer input is handed
+// over inside the XCD.  Per layer:
 //
-//   R  router rows: the waves of each XCD compute every router row once
-//      (the fixed-order dot of the router contract; bf16 rows, or 8-bit
-//      MLX-affine rows with their group scales and biases) and publish it in
-//      that XCD's L2 only; the row weights are loaded before x is even staged
-//   K  every workgroup polls its XCD's logits (an L2 round trip, about half
-//      the latency of the device-coherent hand-overs) and ranks them with the
-//      shared gate's logit, which its wave 0 computes itself (row weights
-//      prefetched like the router rows): 4 keys per lane sorted locally, then
+//   C  the layer input.  Waves 0-3 ("pollers", no prefetched loads in their
+//      queue, so a poll is not served behind them) collect the unit outputs
+//      of their workgroup's rows, sum them in slot order with the previous
+//      layer's scores, add the residual, publish the rows in the XCD's L2 and
+//      collect all of x.  Waves 4-7 ("loaders") load the layer's
+//      routing-independent rows (router rows, the shared gate's row, the
+//      shared pairs, RMSNorm weights) and move the router rows to LDS
+//   R  every wave dots one router row (the router contract's fixed order)
+//      from LDS against x; logits go to the XCD's L2
+//   S  waves 6 and 7: one shared pair each; its activation is published
+//      device-wide after the routed loads are out
+//   K  wave 0 ranks the XCD's logits: 4 keys per lane sorted locally, then
 //      top_k rounds of a DPP wave maximum
-//   G  gate/up pairs: every wave issues the loads of all its pairs and of
-//      its down row of every unit at once (about 110 KB per CU in flight),
-//      computes SwiGLU
-//   D  the down row of every unit from registers, weighted combine, gated
-//      shared expert, residual, bf16 out
+//   G  this XCD's routed expert: two pairs per wave, activations to the
+//      XCD's L2; then eight down rows per wave are loaded
+//   D  the routed rows' dots, and two shared rows per loader wave; the
+//      results go to LDS and one wave stores them after the layer's last
+//      barrier
+//   O  (after the last layer) every workgroup combines 8 output rows
 //
-// The routing-independent loads of the shared expert are issued first.
-//
-// Values handed between workgroups (logits, activations, a chained layer's
-// output) are tagged words, (bf16 value << 16) | (phase & 0xFFFF), written
-// and read with agent-scope atomics.  A consumer polls the data itself until
-// every tag it needs shows the current phase: no separate flag round trip,
-// no same-address atomics (which serialise across CUs), no resets.  The
-// phase base comes from an epoch word read at start; workgroup 0 advances
-// it once per launch after it has consumed a tagged value from every
-// workgroup (every workgroup owns at least one gate/up pair, which the
-// host checks), so every workgroup has read the old epoch by then.  Every
-// wait is bounded: on timeout the kernel sets a status word and still runs
-// to completion.
-#include <stdlib.h>
-
+// Values handed between workgroups are tagged words, (bf16 value << 16) |
+// (phase & 0xFFFF), with the phase epoch + layer + 1 taken from an epoch word
+// read at start.  A consumer polls the data itself until every tag it needs
+// shows the current phase: no separate flag round trip, no same-address
+// atomics (which serialise across CUs), no resets.  XCD-local words are
+// stored with sc0 (to the XCD's L2) and read with sc0 nt; device-wide words
+// with sc1 stores and loads.  Every wait is bounded: on timeout the kernel
+// sets a status word and still runs to completion.
 #include "common.h"
 #include "kernels.h"
 
@@ -44,13 +52,7 @@ namespace {
 constexpr int kThreads = kFusedThreads;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSpinLimit = 1 << 20;
-// Waves that collect the hand-overs for their workgroup: router rows and
-// shared-expert pairs (prefetched for the next layer) sit on waves 0 and 1.
-constexpr int kPollWave = 0;  // logits: a wave that does not poll act
-// x: every wave polls 1/8 of it (one 16-byte piece per lane; measured
-// against 2 and 4 polling waves: 15.4 vs 16.0 and 15.5 us per layer)
-constexpr int kXPollWaves = 8;
-constexpr int kActPollWaves = 6;       // act: waves 2..7
+constexpr int kPollWave = 0;  // ranks the logits and computes the scores
 
 __device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -118,26 +120,6 @@ __device__ __forceinline__ void poll_tagged(const uint32_t* src, int n_words, ui
   }
 }
 
-// wave_sum of N values at once, level by level (the same operations per
-// value as wave_sum, so the same results; the N chains overlap).
-template <int N>
-__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0xB1);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x4E);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x141);
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] += dpp_f(v[i], 0x140);
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    v[i] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[i]), 0x401F));
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 0)) +
-           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), 32));
-}
 
 __device__ __forceinline__ void cswap_desc(uint32_t& a, uint32_t& b) {
   const uint32_t hi = a > b ? a : b;
@@ -208,27 +190,7 @@ struct DownRegs {
   uint32_t w[WPL];
 };
 
-template <int BITS>
-__device__ __forceinline__ uint32_t load_down_param_word(const QW& bank, size_t row, int j) {
-  using S = Shape<BITS>;
-  static_assert(S::I / 64 == 8, "4 words of bf16 per down row");
-  const uint16_t* base = (j < 4 ? bank.s : bank.b) + row * (S::I / 64);
-  return reinterpret_cast<const uint32_t*>(base)[j & 3];
-}
 
-template <int BITS>
-__device__ __forceinline__ void load_down_words(DownRegs<Shape<BITS>::DN_WPL>& r,
-                                                const QW& bank, size_t row, int lane) {
-  using S = Shape<BITS>;
-  const uint32_t* src = bank.w + row * S::DN_WPR + lane * S::DN_WPL;
-  if constexpr (S::DN_WPL == 2) {
-    const uint2 v = *reinterpret_cast<const uint2*>(src);
-    r.w[0] = v.x;
-    r.w[1] = v.y;
-  } else {
-    r.w[0] = src[0];
-  }
-}
 
 // One gate row held in registers by a wave: bf16 (RQ 0: lane chunks
 // lane + 64 i of 8 values) or 8-bit MLX-affine (RQ 1: lane chunks of 16
@@ -247,22 +209,6 @@ struct GateRow<1> {
   uint32_t s[C], b[C];
 };
 
-__device__ __forceinline__ void load_gate_row(GateRow<0>& r, const uint16_t* w, const QW&,
-                                              size_t, int lane) {
-#pragma unroll
-  for (int i = 0; i < GateRow<0>::C; ++i) r.w[i] = load16_stream(w + (lane + 64 * i) * 8);
-}
-__device__ __forceinline__ void load_gate_row(GateRow<1>& r, const uint16_t*, const QW& bank,
-                                              size_t row, int lane) {
-  constexpr int H = kFusedH;
-#pragma unroll
-  for (int i = 0; i < GateRow<1>::C; ++i) {
-    const int ch = lane + 64 * i;
-    r.w[i] = load16_stream(bank.w + row * (H / 4) + ch * 4);
-    r.s[i] = bank.s[row * (H / 64) + (ch >> 2)];
-    r.b[i] = bank.b[row * (H / 64) + (ch >> 2)];
-  }
-}
 
 // This lane's partial of the router contract's dot (x as floats in LDS).
 __device__ __forceinline__ float gate_partial(const GateRow<0>& r, const float* s_x, int lane) {
@@ -323,478 +269,19 @@ __device__ __forceinline__ bool shared_gated(const FusedLayer& L, bool has_share
   return has_shared && (RQ ? L.sgq.w != nullptr : L.sgate_w != nullptr);
 }
 
-// Routing-independent loads of one layer for this wave, in two parts: its
-// router row and its down row of the shared expert (needed first), and its
-// gate/up pairs of the shared expert (unit K).  For a chained layer the
-// first part is issued right after the current layer's routed loads and
-// the second after the current layer's down projection, so neither delays
-// a hand-over.
-template <int BITS, int RQ>
-__device__ __forceinline__ void issue_router_and_shared_down(
-    const FusedLayer& L, int row, int n_rows, bool has_shared, int h, int lane,
-    bool sg_wave, GateRow<RQ>& rw, GateRow<RQ>& sw, DownRegs<Shape<BITS>::DN_WPL>& drs,
-    uint32_t& dpws) {
-  using S = Shape<BITS>;
-  constexpr int H = S::H;
-  if (row < n_rows) load_gate_row(rw, L.router_w + (size_t)row * H, L.rq, (size_t)row, lane);
-  if (sg_wave && shared_gated<RQ>(L, has_shared)) load_gate_row(sw, L.sgate_w, L.sgq, 0, lane);
-  if (has_shared && h < H) {
-    if (lane < 8) dpws = load_down_param_word<BITS>(L.sdn, h, lane);
-    load_down_words<BITS>(drs, L.sdn, h, lane);
-  }
-  issue_fence();
-}
 
-template <int BITS, int CPL, int NP>
-__device__ __forceinline__ void issue_shared_pairs(const FusedLayer& L, bool has_shared, int K,
-                                                   int pw, int n_waves, int n_pairs, int lane,
-                                                   PairRegs<CPL> (&pr)[NP]) {
-  constexpr int I = Shape<BITS>::I;
-  if (has_shared) {
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      const int q = pw + pp * n_waves;
-      if (q < n_pairs && q / I == K) load_pair_params<BITS, CPL>(pr[pp], L.sgu, q - K * I, lane);
-    }
-    issue_fence();
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      const int q = pw + pp * n_waves;
-      if (q < n_pairs && q / I == K) load_pair_words<BITS, CPL>(pr[pp], L.sgu, q - K * I, lane);
-    }
-  }
-  issue_fence();
-}
 
-template <int BITS, int RQ, bool NORM>
-__global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs p) {
-  using S = Shape<BITS>;
-  constexpr int H = S::H;
-  constexpr int I = S::I;
-  constexpr int VPC = S::VPC;
-  constexpr int CPL = S::GU_CPL;
-  constexpr int NP = kMaxFusedPairsPerWave;
-  constexpr int NU = kMaxFusedUnits;
-  constexpr int kStageX = H / kThreads;                     // 4
-  constexpr int kPer = kFusedMaxExperts / 64;               // keys per lane (4)
-  static_assert(kPer == 4, "the local sort network below is for 4 keys per lane");
-  static_assert(H % (256 * kXPollWaves) == 0 && NU * I % (256 * kActPollWaves) == 0,
-                "hand-overs split evenly over the polling waves");
-  const int G = gridDim.x;
-  const int wg = blockIdx.x;
-  const int wave = threadIdx.x >> 6;
-  const int lane0 = threadIdx.x & 63;
-  const int gwave = wg * kWaves + wave;
-  const int n_waves = G * kWaves;
-  const int K = p.K;
-  const int E = p.E;
-  const int U = K + p.has_shared;
-  const int n_pairs = U * I;
-  const int h = gwave;            // one down row per wave (n_waves >= H is checked)
-  const int xcd = wg & 7;
-  // router row of this wave within its XCD (G / 8 workgroups x 8 waves >= E
-  // is checked), if any; the shared gate's row is done by every workgroup
-  const int row = (wg >> 3) + (G >> 3) * wave;
-  // gate/up pairs q = pw + pp * n_waves: the pairs past 2 * n_waves land on
-  // low wave indices of every workgroup, so each CU streams the same bytes
-  const int pw = wg + G * wave;
-  FusedScratch* sc = p.scratch;
 
-  __shared__ float s_x[H];                 // the layer input (and residual)
-  __shared__ float s_n[NORM ? H : 4];      // its RMSNorm, the block's input
-  float* const s_in = NORM ? s_n : s_x;
-  __shared__ float s_act[NU * I];
-  __shared__ int s_idx[NU];
-  __shared__ float s_coef[NU];
-  __shared__ uint32_t s_base;
-
-  // Layer 0's input first (it gates the router), then the prologue loads.
-  uint32_t xin[kStageX];
-#pragma unroll
-  for (int j = 0; j < kStageX; ++j) xin[j] = (uint32_t)p.x[threadIdx.x + j * kThreads] << 16;
-  if (threadIdx.x == 0) s_base = load_coherent_u32(&sc->epoch);
-
-  PairRegs<CPL> pr[NP];
-  DownRegs<S::DN_WPL> dr[NU];      // slot NU-1: the shared unit
-  uint32_t dpw0 = 0, dpw1 = 0;
-  GateRow<RQ> rw, sw;  // router row; shared gate row (wave kPollWave)
-  uint2 nw = make_uint2(0, 0);  // RMSNorm weights of values 4 t .. 4 t + 3
-  {
-    const FusedLayer L0 = layer_desc(p, 0);
-    // the norm weights first: the oldest load is the first one waited for
-    if constexpr (NORM) nw = *reinterpret_cast<const uint2*>(L0.norm_w + 4 * threadIdx.x);
-    issue_router_and_shared_down<BITS, RQ>(L0, row, E, p.has_shared, h, lane0,
-                                           wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
-    issue_shared_pairs<BITS, CPL, NP>(L0, p.has_shared, K, pw, n_waves, n_pairs, lane0, pr);
-  }
-  __syncthreads();
-  const uint32_t base = s_base;
-  uint32_t phase = 0;
-  bool timed_out = false;
-
-  for (int layer = 0; layer < p.n_layers; ++layer) {
-    // An opaque per-iteration copy of the lane index: stops the compiler from
-    // hoisting every per-lane address of the layer out of the loop (which
-    // would keep them live across all layers and spill them).
-    int lane = lane0;
-    asm volatile("" : "+v"(lane));
-    const FusedLayer L = layer_desc(p, layer);
-    const bool first = layer == 0;
-    const bool last = layer == p.n_layers - 1;
-    const uint32_t tag_logit = base + phase + 1;
-    const uint32_t tag_act = base + phase + 2;
-    const uint32_t tag_x = base + phase + 3;  // used when a next layer reads x
-    phase += last ? 2 : 3;
-    const bool sg_row = shared_gated<RQ>(L, p.has_shared);
-
-    // ---- x (bf16 -> fp32 in LDS).  A chained layer collects the previous
-    // layer's tagged output.
-    if (first) {
-#pragma unroll
-      for (int j = 0; j < kStageX; ++j)
-        s_x[threadIdx.x + j * kThreads] = __uint_as_float(xin[j] & 0xFFFF0000u);
-    } else if (wave >= kWaves - kXPollWaves) {
-      poll_tagged<H / 256 / kXPollWaves>(sc->xs[(layer - 1) & 1], H, tag_logit - 1, s_x, lane,
-                                         wave - (kWaves - kXPollWaves), timed_out);
-    }
-    __syncthreads();
-
-    // ---- RMSNorm: every wave sums the squares in the contract's order (8
-    // values per chunk, chunks lane + 64 i, then the butterfly) and gets the
-    // same r; each thread then writes its 4 normalised values.
-    if constexpr (NORM) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < H / 512; ++i) {
-        const float4 a = *reinterpret_cast<const float4*>(s_x + (lane + 64 * i) * 8);
-        const float4 b = *reinterpret_cast<const float4*>(s_x + (lane + 64 * i) * 8 + 4);
-        acc = fmaf(a.x, a.x, acc);
-        acc = fmaf(a.y, a.y, acc);
-        acc = fmaf(a.z, a.z, acc);
-        acc = fmaf(a.w, a.w, acc);
-        acc = fmaf(b.x, b.x, acc);
-        acc = fmaf(b.y, b.y, acc);
-        acc = fmaf(b.z, b.z, acc);
-        acc = fmaf(b.w, b.w, acc);
-      }
-      const float ms = wave_sum(acc) / (float)H;
-      const float r = 1.0f / sqrtf(ms + L.norm_eps);
-      const float4 v = *reinterpret_cast<const float4*>(s_x + 4 * threadIdx.x);
-      *reinterpret_cast<float4*>(s_n + 4 * threadIdx.x) =
-          make_float4(round_bf16(round_bf16(v.x * r) * bf16_lo(nw.x)),
-                      round_bf16(round_bf16(v.y * r) * bf16_hi(nw.x)),
-                      round_bf16(round_bf16(v.z * r) * bf16_lo(nw.y)),
-                      round_bf16(round_bf16(v.w * r) * bf16_hi(nw.y)));
-      __syncthreads();
-    }
-
-    // ---- R: this wave's router row.
-    if (row < E) {
-      const float acc = wave_sum(gate_partial(rw, s_in, lane));
-      if (lane == 0)
-        __builtin_amdgcn_raw_buffer_store_b32(
-            tagged(f32_to_bf16(acc), tag_logit),
-            __builtin_amdgcn_make_buffer_rsrc(sc->logits[xcd], (short)0, E * 4, 0x00020000),
-            row * 4, 0, kXcdStoreAux);
-    }
-
-    // ---- K: poll all logits (wave 0), rank them, publish the selection in
-    // LDS.  The softmax and the scores are only needed by D: wave 0 computes
-    // them after the routed loads are out (below), off the critical path.
-    float lv[kPer];
-    float m_top = 0.0f;
-    uint32_t my = 0, wsg = 0;
-    if (wave == kPollWave) {
-      // lane l holds experts 4 l .. 4 l + 3 (one 16-byte load from the L2)
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          sc->logits[xcd], (short)0, E * 4, 0x00020000);
-      uint32_t w[kPer];
-      for (int spin = 0;; ++spin) {
-        bool ok = true;
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, 0, kXcdLoadAux);
-        w[0] = v.x;
-        w[1] = v.y;
-        w[2] = v.z;
-        w[3] = v.w;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) ok &= 4 * lane + i >= E || tag_ok(w[i], tag_logit);
-        if (__all(ok)) break;
-        if (spin >= kSpinLimit) { timed_out = true; break; }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      uint32_t k[kPer];
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int e = 4 * lane + i;
-        const uint32_t b = w[i] >> 16;
-        lv[i] = bf16_to_f32(b);
-        k[i] = e < E ? ((bf16_order_key(b) << 16) | (0xFFFFu - (uint32_t)e)) : 0u;
-      }
-      // local sort (descending), then top_k rounds of a wave maximum over
-      // the lanes' current heads
-      cswap_desc(k[0], k[1]);
-      cswap_desc(k[2], k[3]);
-      cswap_desc(k[0], k[2]);
-      cswap_desc(k[1], k[3]);
-      cswap_desc(k[1], k[2]);
-      uint32_t sel[NU - 1];
-#pragma unroll
-      for (int j = 0; j < NU - 1; ++j) {
-        sel[j] = 0;
-        if (j < K) {
-          const uint32_t best = wave_max_u32(k[0]);
-          sel[j] = best;
-          if (k[0] == best) {
-            k[0] = k[1];
-            k[1] = k[2];
-            k[2] = k[3];
-            k[3] = 0;
-          }
-        }
-      }
-      m_top = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
-      // slot j is handled by lane j
-#pragma unroll
-      for (int j = 0; j < NU - 1; ++j)
-        if (lane == j) my = sel[j];
-      if (lane < K) s_idx[lane] = (int)(0xFFFFu - (my & 0xFFFFu));
-      if (lane == 0 && p.has_shared) s_idx[K] = 0;
-    }
-    __syncthreads();
-
-    // ---- routed loads: parameters first, then packed words.
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      const int q = pw + pp * n_waves;
-      const int u = q / I;
-      if (q < n_pairs && u < K)
-        load_pair_params<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
-    }
-    if (h < H && (lane >> 3) < K)
-      dpw0 = load_down_param_word<BITS>(L.dn, (size_t)s_idx[lane >> 3] * H + h, lane & 7);
-    issue_fence();
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      const int q = pw + pp * n_waves;
-      const int u = q / I;
-      if (q < n_pairs && u < K)
-        load_pair_words<BITS, CPL>(pr[pp], L.gu, (size_t)s_idx[u] * 2 * I + (q - u * I), lane);
-    }
-    issue_fence();
-
-    // ---- G: gate/up + SwiGLU of this wave's pairs -> tagged act words.
-    // x of this lane's chunks is the same for every pair.
-    float xv[CPL][VPC];
-    float xs[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int ch = lane + 64 * i;
-      xs[i] = 0.0f;
-#pragma unroll
-      for (int v = 0; v < VPC; v += 4) {
-        const float4 f = *reinterpret_cast<const float4*>(s_in + ch * VPC + v);
-        xv[i][v] = f.x;
-        xv[i][v + 1] = f.y;
-        xv[i][v + 2] = f.z;
-        xv[i][v + 3] = f.w;
-      }
-#pragma unroll
-      for (int v = 0; v < VPC; ++v) xs[i] += xv[i][v];
-    }
-#pragma unroll
-    for (int pp = 0; pp < NP; ++pp) {
-      const int q = pw + pp * n_waves;
-      if (q >= n_pairs) continue;  // wave-uniform
-      float au = 0.0f, ag = 0.0f;
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int ch = lane + 64 * i;
-        const int g = (ch * VPC) >> 6;
-        au += param_of(pr[pp].pw, 0, g) * qdot_chunk<BITS>(pr[pp].wu[i], xv[i]) +
-              param_of(pr[pp].pw, 32, g) * xs[i];
-        ag += param_of(pr[pp].pw, 16, g) * qdot_chunk<BITS>(pr[pp].wg[i], xv[i]) +
-              param_of(pr[pp].pw, 48, g) * xs[i];
-      }
-      au = wave_sum(au);
-      ag = wave_sum(ag);
-      if (lane == 0) {
-        const float up = round_bf16(au);
-        const float gate = round_bf16(ag);
-        store_coherent_u32(sc->act + q, tagged(f32_to_bf16(silu(gate) * up), tag_act));
-      }
-      // one pair at a time: keeps the unpacked codes of later pairs from
-      // being hoisted (and spilled) while this one is reduced
-      __builtin_amdgcn_sched_barrier(0);
-    }
-
-    // ---- this wave's down row of every routed unit: issued after the
-    // gate/up math, so the gate/up rows have the memory system to themselves
-    // first; they land while the activations are handed over.
-#pragma unroll
-    for (int u = 0; u < NU - 1; ++u)
-      if (u < K && h < H) load_down_words<BITS>(dr[u], L.dn, (size_t)s_idx[u] * H + h, lane);
-    issue_fence();
-
-    // ---- scores of the selection (wave 0, which does not poll act; read by D):
-    // softmax in fp32 over every expert, probabilities rounded to bf16,
-    // renormalised by the bf16 sum in slot order (mlx-lm's scores.sum(-1) of
-    // bf16 scores), quotient bf16; the shared gate bf16(sigmoid(logit)).
-    if (wave == kPollWave) {
-      // the shared gate's logit (its row is not handed over)
-      if (sg_row) wsg = f32_to_bf16(wave_sum(gate_partial(sw, s_in, lane))) << 16;
-      float z = 0.0f;
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-        if (4 * lane + i < E) z += __expf(lv[i] - m_top);
-      z = wave_sum(z);
-      const float pb =
-          lane < K ? round_bf16(__expf(bf16_to_f32(bf16_from_order_key(my >> 16)) - m_top) / z)
-                   : 0.0f;
-      float total = 0.0f;  // slot order, as the oracle sums
-#pragma unroll
-      for (int j = 0; j < NU - 1; ++j)
-        if (j < K) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), j));
-      if (lane < K) {
-        const float score = p.norm ? round_bf16(pb / round_bf16(total)) : pb;
-        s_coef[lane] = score;
-        if (wg == 0 && last && p.idx_out) {
-          p.idx_out[lane] = (int)(0xFFFFu - (my & 0xFFFFu));
-          p.scores_out[lane] = score;
-        }
-      }
-      if (lane == 0 && p.has_shared)
-        s_coef[K] = sg_row ? round_bf16(sigmoid(bf16_to_f32(wsg >> 16))) : 1.0f;
-    }
-
-    // ---- down scales / biases of every unit, ready before act arrives.
-    const int gd = lane >> 3;
-    float dsc[NU], dbi[NU];
-#pragma unroll
-    for (int uu = 0; uu < NU; ++uu) {
-      dsc[uu] = uu == NU - 1 ? param_of(dpw1, 0, gd) : param_of(dpw0, uu * 8, gd);
-      dbi[uu] = uu == NU - 1 ? param_of(dpw1, 4, gd) : param_of(dpw0, uu * 8 + 4, gd);
-    }
-
-    // ---- collect every act word into LDS.
-    if (wave >= kWaves - kActPollWaves)
-      poll_tagged<NU * I / 256 / kActPollWaves>(sc->act, n_pairs, tag_act, s_act, lane,
-                                                wave - (kWaves - kActPollWaves), timed_out);
-    __syncthreads();
-
-    // The next layer's descriptor (scalar loads) before this layer's output
-    // stores: read after them, it waited for the stores to complete.
-    const FusedLayer Ln = layer_desc(p, last ? layer : layer + 1);
-
-    // ---- D: down row h of every unit from registers.
-    if (h < H) {
-      float ys[NU];
-#pragma unroll
-      for (int uu = 0; uu < NU; ++uu) {
-        // register slot NU-1 holds the shared unit (unit index K)
-        const int u = uu == NU - 1 ? K : uu;
-        const bool on = uu == NU - 1 ? (p.has_shared != 0) : (uu < K);
-        ys[uu] = 0.0f;
-        if (!on) continue;
-        const float4 a0 = *reinterpret_cast<const float4*>(s_act + u * I + lane * 8);
-        const float4 a1 = *reinterpret_cast<const float4*>(s_act + u * I + lane * 8 + 4);
-        const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-        // sum of the lane's 8 activations (the group-affine bias term)
-        const float asum =
-            ((((((a0.x + a0.y) + a0.z) + a0.w) + a1.x) + a1.y) + a1.z) + a1.w;
-        float qa = 0.0f;
-        if constexpr (BITS == 8) {
-          qa = qdot_word8(dr[uu].w[0], a[0], a[1], a[2], a[3], qa);
-          qa = qdot_word8(dr[uu].w[1], a[4], a[5], a[6], a[7], qa);
-        } else {
-          const uint32_t wd = dr[uu].w[0];
-          const uint32_t lo = wd & 0x0F0F0F0Fu;
-          const uint32_t hi = (wd >> 4) & 0x0F0F0F0Fu;
-          qa = fmaf((float)(lo & 0xFFu), a[0], qa);
-          qa = fmaf((float)(hi & 0xFFu), a[1], qa);
-          qa = fmaf((float)((lo >> 8) & 0xFFu), a[2], qa);
-          qa = fmaf((float)((hi >> 8) & 0xFFu), a[3], qa);
-          qa = fmaf((float)((lo >> 16) & 0xFFu), a[4], qa);
-          qa = fmaf((float)((hi >> 16) & 0xFFu), a[5], qa);
-          qa = fmaf((float)(lo >> 24), a[6], qa);
-          qa = fmaf((float)(hi >> 24), a[7], qa);
-        }
-        ys[uu] = dsc[uu] * qa + dbi[uu] * asum;
-      }
-      wave_sum_n<NU>(ys);
-      float acc = 0.0f;
-#pragma unroll
-      for (int uu = 0; uu < NU; ++uu) {
-        const int u = uu == NU - 1 ? K : uu;
-        const bool on = uu == NU - 1 ? (p.has_shared != 0) : (uu < K);
-        if (on) acc += s_coef[u] * round_bf16(ys[uu]);
-      }
-      if (lane == 0) {
-        float o = round_bf16(acc);
-        if (p.residual_mode == 1)
-          o = round_bf16(s_x[h] + o);
-        else if (p.residual_mode == 2)
-          o = round_bf16(bf16_to_f32(p.residual[h]) + o);
-        const uint32_t ob = f32_to_bf16(o);
-        if (last)
-          p.out[h] = (uint16_t)ob;
-        else
-          store_coherent_u32(sc->xs[layer & 1] + h, tagged(ob, tag_x));
-      }
-    }
-    // The next layer's routing-independent loads go out now that this
-    // layer's down rows are done: issued earlier they would sit in front of
-    // the hand-over polls of their wave (a wave's loads return in order).
-    // x is polled by every wave (behind these loads, which land while the
-    // other workgroups finish this layer) and act by waves 2-7; the logits
-    // by wave 0, whose extra loads (shared gate row, shared pairs) are back
-    // by then.
-    if (!last) {
-      if constexpr (NORM) nw = *reinterpret_cast<const uint2*>(Ln.norm_w + 4 * threadIdx.x);
-      issue_router_and_shared_down<BITS, RQ>(Ln, row, E, p.has_shared, h, lane,
-                                             wave == kPollWave, rw, sw, dr[NU - 1], dpw1);
-      issue_shared_pairs<BITS, CPL, NP>(Ln, p.has_shared, K, pw, n_waves, n_pairs, lane, pr);
-    }
-    // s_x / s_act / s_idx are rewritten by the next layer
-    __syncthreads();
-  }
-  if (timed_out) store_coherent_u32(&sc->err, 1u);
-  // Workgroup 0 has consumed an act word from every workgroup, each written
-  // after that workgroup read the epoch: advancing it now is safe.
-  if (wg == 0 && threadIdx.x == 0) store_coherent_u32(&sc->epoch, base + phase);
-}
-
-// ===========================================================================
-// XCD-per-unit layout of the same layer (fused_xcd_kernel).  256 workgroups,
-// 32 per XCD.  Routed slot u (u < K <= 8) is computed whole by XCD u: its
-// gate/up pairs, the SwiGLU activations (handed over inside that XCD's L2)
-// and all of its down rows, written as one bf16 output word per row.  The
-// shared expert does not depend on the routing: XCD x computes its pairs
-// 64 x .. 64 x + 63 right after the router rows (handed over device-wide, off
-// the routed critical path) and its down rows 256 x .. 256 x + 255.  A layer
-// therefore has one device-wide hand-over on its critical path: every XCD
-// combines the unit outputs of its own 2048 rows (each workgroup 64 rows),
-// and the combined layer input is handed over inside the XCD.  Per layer:
-//
-//   C  (layers after the first) combine: poll the unit outputs of this
-//      workgroup's rows, sum them in slot order with the previous layer's
-//      scores, residual, publish in the XCD's L2; every wave polls 1/8 of x
-//   R  router rows, one per wave, logits in the XCD's L2
-//   S  waves 6 and 7: the shared pair of this wave, published device-wide
-//   K  wave 0 ranks the XCD's logits
-//   G  this XCD's routed expert: two pairs per wave, act in the XCD's L2
-//   D  eight routed down rows per wave from registers; one shared down row
-//   O  (after the last layer) every workgroup combines 8 output rows
-//
-// Every word handed over is tagged with the layer's phase (epoch + layer +
-// 1).  Single-buffered XCD-local words (logits, act) are safe because every
-// workgroup of the XCD reads the whole combined x of layer L + 1, written by
-// each of them after it finished layer L.  The unit outputs and the shared
-// activations are double-buffered by layer parity: a workgroup writes layer
-// L's only after it has read every workgroup's shared activations of layer
-// L, which each wrote after reading layer L - 1's combine inputs.  The
-// shared activations are written (as zeros) even without a shared expert,
-// so that workgroup 0, which reads them all, has consumed a word from every
-// workgroup before it advances the epoch.
+// Buffering.  Single-buffered XCD-local words (logits, act) are safe
+// because every workgroup of the XCD reads the whole combined x of layer
+// L + 1, written by each of them after it finished layer L.  The unit
+// outputs, the combined x and the shared activations are double-buffered by
+// layer parity: a workgroup writes layer L's unit outputs only after it has
+// read every workgroup's shared activations of layer L, which each wrote
+// after reading layer L - 1's combine inputs.  The shared activations are
+// written (as zeros) even without a shared expert, so that workgroup 0, which
+// reads them all, has consumed a word from every workgroup before it
+// advances the epoch at the end.
 
 constexpr int kXcds = 8;
 constexpr int kXcdWgs = kFusedXcdGrid / kXcds;           // 32 workgroups per XCD
@@ -997,34 +484,6 @@ __device__ __forceinline__ uint32_t pair_act(const PairRegs<Shape<BITS>::GU_CPL>
   return f32_to_bf16(silu(gate) * up);
 }
 
-// Polls tagged words w[u * stride + r0 .. + 7] of units u < U (agent
-// coherence) into s_y[u][0..7]: lanes 2 u and 2 u + 1 load 16 bytes each.
-__device__ __forceinline__ void poll_unit_rows(const uint32_t* w, int stride, int U, int r0,
-                                               uint32_t tag, float (*s_y)[kXcdRows], int lane,
-                                               bool& timed_out) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(w), (short)0, kMaxFusedUnits * stride * 4, 0x00020000);
-  const int u = lane >> 1, hf = lane & 1;
-  bool pend = lane < 2 * U;
-  const int off = (u * stride + r0 + 4 * hf) * 4;
-  for (int spin = 0;; ++spin) {
-    if (pend) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 16);
-      if (tag_ok(v.x, tag) && tag_ok(v.y, tag) && tag_ok(v.z, tag) && tag_ok(v.w, tag)) {
-        *reinterpret_cast<float4*>(&s_y[u][4 * hf]) =
-            make_float4(__uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y & 0xFFFF0000u),
-                        __uint_as_float(v.z & 0xFFFF0000u), __uint_as_float(v.w & 0xFFFF0000u));
-        pend = false;
-      }
-    }
-    if (!__any(pend)) break;
-    if (spin >= kSpinLimit) {
-      timed_out = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
 
 // out = bf16(sum_u coef[u] * y[u]) in slot order (the shared unit, slot K,
 // last), then the residual: the combine of the one-row-per-wave kernel.
@@ -1208,7 +667,6 @@ __global__ __launch_bounds__(kThreads) void fused_xcd_kernel(const FusedArgs p) 
   const int hs0 = xcd * kXcdWaves + j * kXcdRows + 2 * q;
   const int c_own = j * (kWaves * kXcdRows) + wave * kCombRows;  // combine rows (pollers)
   FusedScratch* sc = p.scratch;
-  const uint32_t sh_rows = has_shared ? 1u : 0u;
 
   __shared__ float s_x[2][H];
   __shared__ float s_n[NORM ? H : 4];
@@ -1590,28 +1048,12 @@ __global__ __launch_bounds__(kThreads) void fused_xcd_kernel(const FusedArgs p) 
 namespace {
 template <int BITS, int RQ>
 const void* fused_fn_n(int norm) {
-  return norm ? (const void*)fused_decode_kernel<BITS, RQ, true>
-              : (const void*)fused_decode_kernel<BITS, RQ, false>;
+  return norm ? (const void*)fused_xcd_kernel<BITS, RQ, true>
+              : (const void*)fused_xcd_kernel<BITS, RQ, false>;
 }
 const void* fused_fn(int bits, int rq8, int norm) {
   if (bits == 8) return rq8 ? fused_fn_n<8, 1>(norm) : fused_fn_n<8, 0>(norm);
   return rq8 ? fused_fn_n<4, 1>(norm) : fused_fn_n<4, 0>(norm);
-}
-template <int BITS, int RQ>
-const void* xcd_fn_n(int norm) {
-  return norm ? (const void*)fused_xcd_kernel<BITS, RQ, true>
-              : (const void*)fused_xcd_kernel<BITS, RQ, false>;
-}
-const void* xcd_fn(int bits, int rq8, int norm) {
-  if (bits == 8) return rq8 ? xcd_fn_n<8, 1>(norm) : xcd_fn_n<8, 0>(norm);
-  return rq8 ? xcd_fn_n<4, 1>(norm) : xcd_fn_n<4, 0>(norm);
-}
-bool xcd_variant() {
-  static const int v = [] {
-    const char* e = getenv("RMOE_FUSED_XCD");
-    return e && e[0] == '0' ? 0 : 1;
-  }();
-  return v != 0;
 }
 }  // namespace
 
@@ -1636,22 +1078,22 @@ hipError_t fused_grid(int bits, int rq8, int norm, int* grid) {
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_fn(bits, rq8, norm),
                                                    kThreads, 0);
   if (e != hipSuccess) return e;
-  *grid = per_cu >= 1 ? (cus < kFusedMaxGrid ? cus : kFusedMaxGrid) : 0;
+  // one workgroup per CU, 32 on each of the 8 XCDs (0: not this device)
+  *grid = per_cu >= 1 && cus >= kFusedXcdGrid ? kFusedXcdGrid : 0;
   if (dev >= 0 && dev < 64) __atomic_store_n(&cache[dev][slot], *grid + 1, __ATOMIC_RELAXED);
   return hipSuccess;
 }
 
 hipError_t launch_fused_decode(const FusedArgs& a, int bits, int grid, hipStream_t s) {
+  if (grid != kFusedXcdGrid) return hipErrorInvalidValue;
   FusedArgs args = a;
   void* kargs[] = {&args};
-  const bool xcd = xcd_variant() && grid >= kFusedXcdGrid;
-  const void* fn = xcd ? xcd_fn(bits, a.rq8, a.rms_norm) : fused_fn(bits, a.rq8, a.rms_norm);
-  if (xcd) grid = kFusedXcdGrid;
+  const void* fn = fused_fn(bits, a.rq8, a.rms_norm);
   // A cooperative launch guarantees every workgroup is resident.  Under
   // stream capture, or when the caller has turned cooperative launches off,
-  // a plain launch of the same one-workgroup-per-CU grid is made instead
-  // (every workgroup fits at once on an otherwise idle device; the bounded
-  // waits turn anything else into a status error).
+  // a plain launch of the same grid is made instead (every workgroup fits at
+  // once on an otherwise idle device; the bounded waits turn anything else
+  // into a status error).
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (!cooperative_launch_enabled() ||
       (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone))
