@@ -630,7 +630,7 @@ __device__ __forceinline__ void load_down_row_buf(DownRegs<Shape<BITS>::DN_WPL>&
 }
 
 template <int BITS, int RQ, bool NORM>
-__global__ __launch_bounds__(kThreads) void fused_xcd_kernel(const FusedArgs p) {
+__global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs p) {
   using S = Shape<BITS>;
   constexpr int H = S::H;
   constexpr int I = S::I;
@@ -1048,8 +1048,8 @@ __global__ __launch_bounds__(kThreads) void fused_xcd_kernel(const FusedArgs p) 
 namespace {
 template <int BITS, int RQ>
 const void* fused_fn_n(int norm) {
-  return norm ? (const void*)fused_xcd_kernel<BITS, RQ, true>
-              : (const void*)fused_xcd_kernel<BITS, RQ, false>;
+  return norm ? (const void*)fused_decode_kernel<BITS, RQ, true>
+              : (const void*)fused_decode_kernel<BITS, RQ, false>;
 }
 const void* fused_fn(int bits, int rq8, int norm) {
   if (bits == 8) return rq8 ? fused_fn_n<8, 1>(norm) : fused_fn_n<8, 0>(norm);
