@@ -462,6 +462,9 @@ def main():
             "value": round(us, 1), "unit": "us/layer/token", "cores": threads, "kind": "port",
             "sample": f"oracle/cpu_moe.c block contract (fp32, OpenMP) on layer 0 of the "
                       f"stack, {n} batch-1 tokens with residual, median",
+            # the oracle unpacks one code at a time (a scalar restatement, not
+            # a tuned CPU kernel): its rate over the layer's bytes, for scale
+            "effective_gbps": round(layer_bytes(2048, 512, 256, 8, 8, residual=True) / (us * 1e3), 2),
         }
     print(json.dumps(out), flush=True)
     return 0
