@@ -262,3 +262,39 @@ def test_one_token_top9_without_shared_expert(torch_cuda, bits):
     assert np.array_equal(gidx, ref_idx)
     got = np.concatenate(outs)
     assert _contract_mismatches(got, ref) <= got.size // 500
+
+
+@pytest.mark.parametrize("top_k,shared,experts,bits", [
+    (1, True, 64, 8), (2, False, 32, 4), (4, False, 128, 8), (6, True, 256, 4)])
+def test_one_token_fewer_routed_slots(torch_cuda, top_k, shared, experts, bits):
+    """The single-launch kernel with fewer than eight routed slots: XCDs
+    past the last slot compute no routed expert (only their share of the
+    shared expert, or zero activations without one).  One-token calls and a
+    three-layer chain of the same shape match the oracle; routing exact."""
+    torch = torch_cuda
+    from runnel_amd import native
+    from helpers import layer_to_dev
+    Ls = [M.make_layer(7950 + 10 * top_k + l, hidden=2048, inter=512, experts=experts,
+                       top_k=top_k, bits=bits, shared=shared) for l in range(3)]
+    hs = [layer_to_dev(L) for L in Ls]
+    xs = M.make_x(7951 + top_k, 3, 2048)
+    ws = torch.zeros(hs[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    outs, idxs = [], []
+    for t in range(3):
+        o, i, _ = native.moe_block(hs[0], dev_bf16(xs[t:t + 1]), return_routing=True,
+                                   workspace=ws)
+        outs.append(host_bf16(o))
+        idxs.append(i.cpu().numpy())
+    y = native.moe_chain(native.Chain(hs), dev_bf16(xs[:1]), workspace=ws)
+    torch.cuda.synchronize()
+    assert native.workspace_status(ws) == 0
+    ref, ref_idx, _ = M.block_forward(Ls[0], xs)
+    assert np.array_equal(np.concatenate(idxs), ref_idx)
+    got = np.concatenate(outs)
+    assert _contract_mismatches(got, ref) <= got.size // 500
+    cur = xs[:1]
+    for L in Ls:
+        cur, _, _ = M.block_forward(L, cur, residual_bits=cur)
+    g, r = M.bf16_to_f32(host_bf16(y)), M.bf16_to_f32(cur)
+    assert np.abs(g - r).max() <= MAX_ABS
+    assert cosine(g, r) >= MIN_COS
