@@ -695,10 +695,13 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 
   // Loader waves: every routing-independent load of layer L (unconditional,
   // sized to zero where a part is absent).
-  auto prefetch = [&](const FusedLayer& L, int lane) {
+  auto fetch_router = [&](const FusedLayer& L, int lane) {
     const int r0 = j + kXcdWgs * (2 * q), r1 = j + kXcdWgs * (2 * q + 1);
     load_gate_rows<RQ>(ld.g[0], L.router_w, L.rq, r0 < E ? r0 : E - 1, E, lane);
     load_gate_rows<RQ>(ld.g[1], L.router_w, L.rq, r1 < E ? r1 : E - 1, E, lane);
+    issue_fence();
+  };
+  auto prefetch = [&](const FusedLayer& L, int lane) {
     if (q == 1) {
       const bool sg = shared_gated<RQ>(L, has_shared);
       load_gate_rows<RQ>(ld.g[2], L.sgate_w, L.sgq, 0, sg ? 1 : 0, lane);
@@ -742,6 +745,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         s_x[0][threadIdx.x + jj * kThreads] = __uint_as_float(xin[jj] & 0xFFFF0000u);
     }
     if (loader) {
+      if (layer == 0) fetch_router(L, lane);
       prefetch(L, lane);
       store_gate_row_lds<RQ>(s_rw[2 * q], ld.g[0], lane);
       store_gate_row_lds<RQ>(s_rw[2 * q + 1], ld.g[1], lane);
@@ -929,6 +933,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         issue_fence();
       }
     }
+
+    // The next layer's router rows: issued inside the routed stream rather
+    // than at the next layer's start, where they would queue in front of
+    // the device-wide unit-output poll (13.45 -> 13.09 us per layer).
+    if (loader && !last) fetch_router(layer_desc(p, layer + 1), lane);
 
     // ---- scores (wave 0), as in the one-row-per-wave kernel; the shared
     // gate's row comes from LDS.
