@@ -67,10 +67,6 @@ constexpr int kMaxFusedUnits = kMaxFusedRouted + 1;  // plus the shared expert
 constexpr int kFusedMaxExperts = 256;       // one router row per wave of an XCD
 constexpr int kFusedH = 2048;
 constexpr int kFusedI = 512;
-// Routed down rows issued with the gate/up rows (true) or after the gate/up
-// math (false: the gate/up rows of later waves do not queue behind the down
-// rows of earlier ones; 13.72 -> 13.47 us per layer on the 40-layer chain).
-constexpr bool kFusedXcdDownEarly = false;
 // ---- few-token decode (decode.hip): 2..8 tokens at the shapes above.
 constexpr int kFewMaxTokens = 8;
 
