@@ -78,6 +78,25 @@ def recorded_traffic(layers: int, bits: int):
     return None
 
 
+def recorded_mfma_busy(tokens: int):
+    """Matrix-core busy fractions of the two prefill GEMMs (gate/up, down) as
+    recorded by the rocprofv3 SQ counter passes under profiles/ for this
+    workload (SQ_VALU_MFMA_BUSY_CYCLES over the GRBM-active cycles of every
+    SIMD), or None when no recording exists.  A recorded figure, beside the
+    live flop-rate fraction `mfma_frac`."""
+    f = ROOT / "profiles" / f"prefill{tokens}_mfma.txt"
+    if not f.exists():
+        return None
+    out, kernel = {"file": str(f.relative_to(ROOT))}, None
+    for line in f.read_text().splitlines():
+        if line.startswith("## ") and "prefill_gemm_kernel" in line:
+            kernel = "down" if ", 1>" in line else "gate_up"
+        elif kernel and "-> MFMA busy" in line:
+            out[kernel] = round(float(line.rsplit(None, 1)[1].rstrip("%")) / 100.0, 4)
+            kernel = None
+    return out if len(out) == 3 else None
+
+
 def calibrate_copy(torch, gib: int = 1, reps: int = 5):
     """A plain copy kernel of known size for scaling the counters: each
     launch reads `gib` GiB and writes `gib` GiB (bitwise NOT of int32)."""
@@ -328,6 +347,7 @@ def run_prefill(torch, tokens, bits, skewed, steps, warmup, seed=7):
         "tokens_per_s": round(tokens / (us * 1e-6), 1),
         "tflops": round(flops / (us * 1e-6) / 1e12, 1),
         "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "mfma_busy_recorded": recorded_mfma_busy(tokens),
         "hbm_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
         "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes": nbytes, "flops": flops,
