@@ -7,8 +7,9 @@ weights seeded per layer, 34.4 GB resident in HBM), one batch-1 decode token
 chained through all 40 layers with a residual add between them.  A step is
 one token through the 40 layers in a single launch of the chained kernel
 (rmoe_moe_chain), replayed from a captured HIP graph as a serving loop would
-(--launch eager calls the library every step instead).  Each step's input is
-the previous step's output, so the routing changes from token to token.
+(--launch eager calls the library every step instead, with plain launches;
+eager-cooperative with cooperative ones).  Each step's input is the previous
+step's output, so the routing changes from token to token.
 
 Prints one JSON line.  `value` is microseconds per MoE layer per token
 (lower is better); `hbm_gbps` is the algorithmic bytes of a layer divided
@@ -63,16 +64,15 @@ def layer_bytes(hidden, inter, experts, top_k, bits, shared=True, tokens=1, resi
     return b
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "fused_decode_chain40_q8_traffic.txt"
-
-
 def recorded_traffic(layers: int, bits: int):
     """HBM bytes per launch of the chained decode kernel as measured by the
-    rocprofv3 counter passes recorded under profiles/, or None when no
-    measurement of this exact workload is recorded."""
-    if not TRAFFIC_FILE.exists() or (layers, bits) != (40, 8):
+    rocprofv3 counter passes recorded under profiles/
+    (fused_decode_chain40_q{bits}_traffic.txt), or None when no measurement
+    of this exact workload is recorded."""
+    f = ROOT / "profiles" / f"fused_decode_chain40_q{bits}_traffic.txt"
+    if not f.exists() or layers != 40:
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in f.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch"):
             return int(line.split("=")[1].strip())
     return None
@@ -199,8 +199,7 @@ def run_decode_chain(args, torch):
         native.moe_chain(chain, bufs[i & 1], out=bufs[(i + 1) & 1], workspace=ws)
 
     step = launch
-    if args.launch == "eager-plain":
-        native.set_cooperative_launch(False)
+    native.set_cooperative_launch(args.launch == "eager-cooperative")
     if args.launch == "graph":
         # the decode loop as a serving loop runs it: one captured HIP graph
         # per direction of the ping-pong buffers, each holding the one
@@ -244,6 +243,68 @@ def run_decode_chain(args, torch):
         "us_layer": us_layer, "us_token": us_token, "step_us": step_us, "gbps": gbps,
         "layer_bytes": lbytes, "resident_gb": sum(lw.nbytes() for lw in stack) / 1e9,
         "gen_s": gen_s, "wall_s": wall, "stack": stack,
+    }
+
+
+def run_decode_single(torch, bits, copies=16, calls=64, reps=20, warmup=3, seed0=1000):
+    """One MoE layer per call at batch-1 decode (rmoe_moe_block, one token:
+    the single-launch kernel with one layer), the single-layer workloads of
+    the metric (8-bit and 4-bit).  `calls` calls with seeded inputs x_t ~
+    N(0, 1) go round `copies` independently seeded copies of the layer, so
+    that the experts a call reads (31 MB at 8 bits) were not read by the
+    calls just before it: together the calls touch far more than the 256 MB
+    memory-side cache.  The calls are captured in one HIP graph and
+    replayed; HIP events around `reps` replays.  Also reported: the same
+    layer and input every call (`us_cached`), whose 31 MB then stay in the
+    memory-side cache."""
+    from runnel_amd import native, synthetic
+    H = 2048
+    layers = [synthetic.make_layer(seed0 + c, bits=bits) for c in range(copies)]
+    hs = [lw.handle() for lw in layers]
+    xs = synthetic.make_x(seed0 + 7, calls, H)
+    outs = torch.empty_like(xs)
+    ws = torch.zeros(hs[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+
+    def timed(schedule):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for t, c in schedule:
+                native.moe_block(hs[c], xs[t:t + 1], out=outs[t:t + 1], workspace=ws,
+                                 check=False)
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) * 1000.0 / (reps * len(schedule))
+
+    us = timed([(t, t % copies) for t in range(calls)])
+    us_cached = timed([(0, 0)] * calls)
+    status = native.workspace_status(ws)
+    if status != 0:
+        raise RuntimeError(f"single-layer decode reported status {status}")
+    nbytes = layer_bytes(H, 512, 256, 8, bits)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    del layers, hs
+    return {
+        "workload": f"one {bits}-bit MoE layer per call, batch-1 decode (hidden 2048, 256 "
+                    "experts, top-8 + shared, inter 512, group 64)",
+        "us_per_layer": round(us, 3), "tokens_per_s": round(1e6 / us, 1),
+        "us_cached": round(us_cached, 3),
+        "calls": calls, "layer_copies": copies,
+        "launch": f"graph of {calls} single-layer calls",
+        "roofline": {
+            "bound": "hbm", "kernel": "fused_decode_kernel (one layer per launch)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "bytes_per_launch": nbytes, "us_per_launch": round(us, 3),
+        },
     }
 
 
@@ -372,10 +433,11 @@ def main():
                          "(h + MoE(RMSNorm(h)), the decoder's sequence)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--launch", choices=["graph", "eager", "eager-plain"], default="graph",
+    ap.add_argument("--launch", choices=["graph", "eager", "eager-cooperative"],
+                    default="graph",
                     help="replay captured HIP graphs (default), launch eagerly every "
-                         "step (cooperative launch), or eagerly with plain launches "
-                         "(rmoe_set_cooperative_launch(0))")
+                         "step (plain launches, the library's default), or eagerly "
+                         "with cooperative launches (rmoe_set_cooperative_launch(1))")
     ap.add_argument("--workload", choices=["decode40", "prefill512", "prefill8192", "few"],
                     default="decode40",
                     help="decode40: the bench line; the prefill workloads and few "
@@ -385,6 +447,9 @@ def main():
                     help="token counts of --workload few (comma-separated)")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the prefill figures appended to the decode line")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the 4-bit chain and the single-layer decode figures "
+                         "appended to the decode line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the plain copy kernel used to scale HBM counters")
     args = ap.parse_args()
@@ -461,17 +526,48 @@ def main():
             "frac_of_measured_read": round(achieved / read_gbps, 4),
         },
     }
-    if args.bits == 8 and args.gate_bits is None and not args.post_norm:
+    default_line = args.bits == 8 and args.gate_bits is None and not args.post_norm
+    if default_line:
         # 4 tokens per call through the same 40 layers (the few-token kernels)
         out["few_token"] = run_few_tokens(torch, res["stack"], 4)
+    if default_line and not args.no_extra:
+        # the same chain with 4-bit experts (its own stack, freed after)
+        a4 = argparse.Namespace(**vars(args))
+        a4.bits = 4
+        r4 = run_decode_chain(a4, torch)
+        b4 = r4["layer_bytes"] * args.layers
+        ach4 = b4 / (r4["us_token"] * 1e-6) / 1e9
+        out["decode40_4bit"] = {
+            "workload": f"{args.layers}-layer 4-bit MoE chain, batch-1 decode with residual",
+            "us_per_layer": round(r4["us_layer"], 3),
+            "tokens_per_s": round(1e6 / r4["us_token"], 2),
+            "roofline": {
+                "bound": "hbm", "kernel": "fused_decode_kernel (whole chain in one launch)",
+                "achieved": round(ach4, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(ach4 / HBM_PEAK_GBPS, 4),
+                "traffic": recorded_traffic(args.layers, 4),
+                "bytes_per_launch": b4, "us_per_launch": round(r4["us_token"], 3),
+            },
+        }
+        del r4
+        # one layer per call at 8 and 4 bits, rotating over 16 copies
+        out["decode_1layer_8bit"] = run_decode_single(torch, 8)
+        out["decode_1layer_4bit"] = run_decode_single(torch, 4)
     if not args.no_prefill:
         # prefill figures of the same build (one layer per call, HIP events)
         # enough warm-up calls for the clocks to settle: three back-to-back
         # rounds of 13 calls measured 904, 815 and 792 us at 8192 tokens
+        p512 = run_prefill(torch, 512, 8, False, 20, 40)
+        p8k = run_prefill(torch, 8192, 4, True, 20, 30)
+        # flat numbers (tokens/s, microseconds, roofline fractions), then
+        # each run's full record
         out["prefill"] = {
-            "512 tokens 8-bit": run_prefill(torch, 512, 8, False, 20, 40),
-            "8192 tokens 4-bit zipf": run_prefill(torch, 8192, 4, True, 20, 30),
+            "tok_s_512tok_8bit": p512["tokens_per_s"], "us_512tok_8bit": p512["us"],
+            "hbm_frac_512tok_8bit": p512["hbm_frac"],
+            "tok_s_8192tok_4bit_zipf": p8k["tokens_per_s"], "us_8192tok_4bit_zipf": p8k["us"],
+            "mfma_frac_8192tok_4bit_zipf": p8k["mfma_frac"],
         }
+        out["prefill_runs"] = [p512, p8k]
     if not args.no_cpu_baseline:
         from oracle.moe_ref import f32_to_bf16
         lw0 = res["stack"][0]

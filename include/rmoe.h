@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define RMOE_ABI_VERSION 4
+#define RMOE_ABI_VERSION 5
 
 #define RMOE_OK 0
 #define RMOE_EINVAL (-1) /* inconsistent or unsupported shape / argument */
@@ -58,10 +58,13 @@ extern "C" {
 #define RMOE_EWS (-4)    /* workspace missing or too small */
 #define RMOE_EHIP (-5)   /* the HIP runtime reported an error */
 #define RMOE_ENULL (-6)  /* a required pointer is NULL */
-/* Not returned by any call (the calls do not wait for the GPU): the code
+/* Not returned by any call (the calls do not wait for the GPU): the codes
  * callers report when a workspace's status word (rmoe_workspace_status_offset)
- * shows that a single-launch decode gave up a cross-workgroup wait. */
+ * is 1 (a single-launch decode gave up a cross-workgroup wait, or the call
+ * was cancelled) or 2 (a workgroup read an XCC id outside 0-7, so it could
+ * not take part in the XCD-local hand-overs). */
 #define RMOE_ETIMEOUT (-7)
+#define RMOE_EPLACEMENT (-8)
 
 /* One MLX-affine quantized bank: w [experts, rows, cols*bits/32] u32,
  * scales / biases [experts, rows, cols/group_size] bf16. */
@@ -262,21 +265,31 @@ int rmoe_moe_chain(const rmoe_layer* layer0, const void* device_table,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Byte offset inside a workspace of a uint32 status word: nonzero when a
- * single-launch decode timed out waiting for another workgroup (the call
- * still completes; its outputs are then not valid). */
+ * single-launch decode failed (the call still completes; its outputs are then
+ * not valid): 1 when a workgroup gave up a cross-workgroup wait (every wait
+ * is bounded, and the other workgroups of the call stop waiting as soon as
+ * one gives up), 2 when a workgroup read an XCC id outside 0-7.  The word is
+ * sticky: later calls leave it set until the caller
+ * clears it.  The uint32 before it holds the workspace's phase epoch and the
+ * one after it the abort word: a caller cancels the next single-launch call
+ * on the workspace before it runs by writing epoch + 1 there (the call then
+ * waits for nothing and sets the status word to 1). */
 size_t rmoe_workspace_status_offset(void);
 
 /* Launch mode of the single-launch decode kernel (rmoe_moe_block with one
  * token of the decode shape, rmoe_moe_chain) outside stream capture.
- * enabled = 1 (the default): a cooperative launch, which guarantees every
- * workgroup is resident whatever else runs on the device, but does not
- * overlap the previous call (about 17 us more per call on MI355X).
- * enabled = 0: a plain launch, as stream capture records it; valid while no
- * other work runs on the device during the call (a workgroup left waiting
- * for one that is not resident times out and sets the status word above).
- * Process-wide; returns the previous mode.  No counterpart in the
- * reference (its probes submit one Metal command buffer per call): for
- * eager decode loops that own the device. */
+ * enabled = 0 (the default): a plain launch, as stream capture records it
+ * (a one-token layer call takes about 14 us back to back on MI355X);
+ * workgroups that wait for others that are not yet resident (kernels of
+ * other streams holding CUs) wait until those run, and two single-launch
+ * calls that overlap on different streams can each hold CUs the other
+ * needs: their waits then give up and set the status word above.
+ * enabled = 1: a cooperative launch, which guarantees every workgroup is
+ * resident whatever else runs on the device, but does not overlap the
+ * previous call (about 18 us more per call), for callers that run such
+ * calls on several streams at once.  Process-wide; returns the previous
+ * mode.  No counterpart in the reference (its probes submit one Metal
+ * command buffer per call). */
 int rmoe_set_cooperative_launch(int32_t enabled);
 
 /* Affine quantization of fp32 rows [rows, cols] (group_size 64, bits 4|8):

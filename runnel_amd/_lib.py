@@ -21,8 +21,9 @@ RMOE_EWS = -4
 RMOE_EHIP = -5
 RMOE_ENULL = -6
 RMOE_ETIMEOUT = -7
+RMOE_EPLACEMENT = -8
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 EXPORTED = (
     "rmoe_abi_version", "rmoe_last_error", "rmoe_status_string",

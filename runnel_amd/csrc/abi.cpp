@@ -19,7 +19,7 @@ static_assert(RMOE_NOALLOC_SCRATCH_BYTES == rmoe::kStaticScratchBytes,
 namespace {
 
 thread_local std::string g_error;
-std::atomic<int> g_cooperative{1};  // rmoe_set_cooperative_launch
+std::atomic<int> g_cooperative{0};  // rmoe_set_cooperative_launch (plain by default)
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -512,6 +512,8 @@ const char* rmoe_status_string(int status) {
     case RMOE_EHIP: return "HIP runtime error";
     case RMOE_ENULL: return "NULL pointer";
     case RMOE_ETIMEOUT: return "single-launch decode timed out (outputs not valid)";
+    case RMOE_EPLACEMENT:
+      return "single-launch decode: XCC id outside 0-7 (outputs not valid)";
     default: return "unknown status";
   }
 }
@@ -755,16 +757,16 @@ int rmoe_moe_block_noalloc(const rmoe_layer* L, const uint16_t* x, int32_t token
                 "library's static scratch; use rmoe_moe_block with a workspace",
                 need, rmoe::kStaticScratchBytes);
   void* ws = nullptr;
-  hipError_t e = rmoe::static_scratch(&ws);
+  hipError_t e = rmoe::static_scratch(static_cast<hipStream_t>(stream), &ws);
   if (e != hipSuccess) return hip_fail(e, "static scratch address");
   if ((rc = block_launch(L, x, tokens, residual, out, indices_out, scores_out, ws, stream)))
     return rc;
-  if (status_out) {
-    e = rmoe::launch_take_status(
-        reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + rmoe_workspace_status_offset()),
-        status_out, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail(e, "status launch");
-  }
+  // the status word is taken (and cleared) after every call, so that a
+  // later call never reports an earlier call's status as its own
+  e = rmoe::launch_take_status(
+      reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + rmoe_workspace_status_offset()),
+      status_out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "status launch");
   return ok();
 }
 

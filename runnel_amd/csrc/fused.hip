@@ -1,9 +1,14 @@
 // Single-launch batch-1 decode of one or more MoE layers (gfx950).
 //
-// 256 workgroups of 8 waves, one per CU and 32 on each of the 8 XCDs
-// (workgroup i runs on XCD i % 8), launched cooperatively so that every
-// workgroup is resident (inside a captured graph: a plain launch of the same
-// grid, see launch_fused_decode).  Routed slot u (u < K <= 8) is computed
+// 256 workgroups of 8 waves, one per CU and 32 on each of the 8 XCDs,
+// launched cooperatively so that every workgroup is resident (inside a
+// captured graph: a plain launch of the same grid, see launch_fused_decode).
+// A workgroup takes its XCD from the hardware (HW_REG_XCC_ID): the
+// dispatcher deals the workgroups of a launch to the XCDs in turn, but the
+// XCD that receives workgroup 0 follows the launches before it (a plain
+// launch right behind a 7-workgroup kernel on the same queue started on
+// XCD 7), so workgroup i is the (i / 8)-th of its XCD, not necessarily on
+// XCD i % 8.  Routed slot u (u < K <= 8) is computed
 // whole by XCD u: its gate/up pairs, the SwiGLU activations (handed over
 // inside that XCD's L2) and all of its down rows, one bf16 output word per
 // row.  The shared expert does not depend on the routing: XCD x computes its
@@ -36,13 +41,26 @@
 //   O  (after the last layer) every workgroup combines 8 output rows
 //
 // Values handed between workgroups are tagged words, (bf16 value << 16) |
-// (phase & 0xFFFF), with the phase epoch + layer + 1 taken from an epoch word
-// read at start.  A consumer polls the data itself until every tag it needs
-// shows the current phase: no separate flag round trip, no same-address
-// atomics (which serialise across CUs), no resets.  XCD-local words are
-// stored with sc0 (to the XCD's L2) and read with sc0 nt; device-wide words
-// with sc1 stores and loads.  Every wait is bounded: on timeout the kernel
-// sets a status word and still runs to completion.
+// tag, where the tag of phase epoch + layer + 1 (the epoch word is read at
+// start) is phase % 65535 + 1: never 0, the tag of zero-filled scratch.  A
+// consumer polls the data itself until every tag it needs shows the current
+// phase: no separate flag round trip, no same-address atomics (which
+// serialise across CUs), no resets.  Every hand-over word is written by its
+// producer in every layer whatever the call's shape (zeros where a slot is
+// unused), so a word is never older than the previous call and an old word
+// cannot carry the current tag.  XCD-local words are stored with sc0 (to the
+// XCD's L2) and read with sc0 nt; device-wide words with sc1 stores and
+// loads.
+//
+// Every wait is bounded.  A wait gives up after kSpinLimit rounds, or when
+// the call's abort word shows that another workgroup gave up a wait (read
+// every kAbortCheck rounds); the workgroup that gives up publishes the
+// abort word and the status word (1) at once, and a wave that gave up skips
+// its later waits, so a failed call ends promptly and still runs to
+// completion.  A workgroup whose hardware XCC id is not below 8 sets the
+// status word to 2 and the abort word.  A call whose key the host has
+// written into the abort word beforehand waits for nothing and sets the
+// status word to 1 (a cancelled call).
 #include "common.h"
 #include "kernels.h"
 
@@ -53,6 +71,7 @@ namespace {
 constexpr int kThreads = kFusedThreads;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSpinLimit = 1 << 20;
+constexpr int kAbortCheck = 64;  // rounds between reads of the abort word
 constexpr int kPollWave = 0;  // ranks the logits and computes the scores
 
 __device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
@@ -68,7 +87,34 @@ __device__ __forceinline__ uint32_t tagged(uint32_t bf16_bits, uint32_t tag) {
 __device__ __forceinline__ bool tag_ok(uint32_t word, uint32_t tag) {
   return (word & 0xFFFFu) == (tag & 0xFFFFu);
 }
-// XCD-local hand-over (workgroup i runs on XCD i % 8): stores reach the
+// Tag of a phase: 1 .. 65535 (0 is the tag of zero-filled scratch).
+__device__ __forceinline__ uint32_t phase_tag(uint32_t phase) { return phase % 65535u + 1u; }
+
+// State of one wave's bounded waits in one call: the call's abort key (its
+// first phase, never 0) and whether the wave has given up.
+struct WaitState {
+  FusedScratch* sc;
+  uint32_t key;
+  bool gave_up;
+};
+__device__ __forceinline__ void publish_failure(FusedScratch* sc, uint32_t key, uint32_t status) {
+  __hip_atomic_fetch_max(&sc->err, status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&sc->abort, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Called after a round that left words pending: true when the wave stops
+// waiting (round limit, or another workgroup gave up a wait of this call).
+__device__ __forceinline__ bool give_up(WaitState& w, int spin) {
+  const bool stop =
+      spin >= kSpinLimit ||
+      ((spin & (kAbortCheck - 1)) == kAbortCheck - 1 &&
+       __hip_atomic_load(&w.sc->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == w.key);
+  if (stop) {
+    if (!w.gave_up) publish_failure(w.sc, w.key, 1u);
+    w.gave_up = true;
+  }
+  return stop;
+}
+// XCD-local hand-over (between workgroups on one XCD): stores reach the
 // XCD's L2 (the vector L1 writes through); loads with sc0 nt skip the L1
 // and are served by that L2.  Only valid between workgroups of one XCD.
 constexpr int kXcdLoadAux = 3;   // sc0 | nt
@@ -83,7 +129,7 @@ constexpr int kXcdStoreAux = 1;  // sc0
 // polling traffic to one stream per workgroup.
 template <int NL, int AUX = 16>
 __device__ __forceinline__ void poll_tagged(const uint32_t* src, int n_words, uint32_t tag,
-                                            float* dst, int lane, int part, bool& timed_out) {
+                                            float* dst, int lane, int part, WaitState& ws) {
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(src), (short)0, n_words * 4, 0x00020000);
   // this wave's pieces: j0 + j, j < NL (16 bytes per lane each)
@@ -92,6 +138,7 @@ __device__ __forceinline__ void poll_tagged(const uint32_t* src, int n_words, ui
 #pragma unroll
   for (int j = 0; j < NL; ++j)
     if ((lane + 64 * (j0 + j)) * 4 < n_words) pend |= 1u << j;
+  if (ws.gave_up) pend = 0;
   for (int spin = 0;; ++spin) {
     u32x4 v[NL];
 #pragma unroll
@@ -113,10 +160,7 @@ __device__ __forceinline__ void poll_tagged(const uint32_t* src, int n_words, ui
       }
     }
     if (!__any(pend != 0u)) break;
-    if (spin >= kSpinLimit) {
-      timed_out = true;
-      break;
-    }
+    if (give_up(ws, spin)) break;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -655,8 +699,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   const int wg = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane0 = threadIdx.x & 63;
-  const int xcd = wg & 7;  // workgroup i runs on XCD i % 8
-  const int j = wg >> 3;   // workgroup within the XCD
+  // this workgroup's XCD (HW_REG_XCC_ID, hardware register 20, bits 3:0)
+  const uint32_t hw_xcc = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((3 << 11) | 20));
+  const int xcd = (int)(hw_xcc & 7u);
+  const int j = wg >> 3;   // workgroup within the XCD (the XCDs are dealt in turn)
   const int K = p.K;
   const int E = p.E;
   const bool has_shared = p.has_shared != 0;
@@ -684,13 +730,16 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   __shared__ uint32_t s_yo[kWaves * kXcdRows + kXcdRows];  // this layer's unit outputs
   __shared__ int s_idx[NU];
   __shared__ float s_coef[NU];
-  __shared__ uint32_t s_base;
+  __shared__ uint32_t s_base, s_abort;
 
   uint32_t xin[kStageX];
 #pragma unroll
   for (int jj = 0; jj < kStageX; ++jj)
     xin[jj] = (uint32_t)p.x[threadIdx.x + jj * kThreads] << 16;
-  if (threadIdx.x == 0) s_base = load_coherent_u32(&sc->epoch);
+  if (threadIdx.x == 0) {
+    s_base = load_coherent_u32(&sc->epoch);
+    s_abort = load_coherent_u32(&sc->abort);
+  }
 
   PairRegs<CPL> pr[kRoutedPairs];
   PairRegs<CPL> spr;
@@ -732,7 +781,17 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   };
   __syncthreads();
   const uint32_t base = s_base;
-  bool timed_out = false;
+  WaitState wst{sc, base + 1, false};
+  if (hw_xcc >= (uint32_t)kXcds) {
+    wst.gave_up = true;
+    if (threadIdx.x == 0) publish_failure(sc, wst.key, 2u);
+  }
+  // A call whose key is already in the abort word (set by the host to cancel
+  // the call before it runs) waits for nothing and reports status 1.
+  if (s_abort == wst.key) {
+    wst.gave_up = true;
+    if (threadIdx.x == 0) publish_failure(sc, wst.key, 1u);
+  }
 
   for (int layer = 0; layer < p.n_layers; ++layer) {
     int lane = lane0;
@@ -740,7 +799,8 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     const FusedLayer L = layer_desc(p, layer);
     const bool last = layer == p.n_layers - 1;
     const int cur = layer & 1;
-    const uint32_t tag = base + 1 + layer;
+    const uint32_t tag = phase_tag(base + 1 + layer);
+    const uint32_t prev_tag = phase_tag(base + layer);
     const bool sg_row = shared_gated<RQ>(L, has_shared);
 
     // ---- C: the layer input.  Pollers combine their rows of the previous
@@ -769,13 +829,15 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       {
         const __amdgpu_buffer_rsrc_t rs = rsrc(sc->ys[cur ^ 1][0], NU * H * 4);
         const int u = lane >> 2, pc = lane & 3;
-        bool pend = lane < 4 * U;
-        const int off = (u * H + c_own + 4 * pc) * 4;
+        bool pend = lane < 4 * U && !wst.gave_up;
+        // unit u of the combine: routed slot u, or the shared expert's slot
+        const int slot = u < K ? u : kMaxFusedRouted;
+        const int off = (slot * H + c_own + 4 * pc) * 4;
         for (int spin = 0;; ++spin) {
           if (pend) {
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kSc1);
-            if (tag_ok(v.x, tag - 1) && tag_ok(v.y, tag - 1) && tag_ok(v.z, tag - 1) &&
-                tag_ok(v.w, tag - 1)) {
+            if (tag_ok(v.x, prev_tag) && tag_ok(v.y, prev_tag) && tag_ok(v.z, prev_tag) &&
+                tag_ok(v.w, prev_tag)) {
               *reinterpret_cast<float4*>(&s_y[wave][u][4 * pc]) = make_float4(
                   __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y & 0xFFFF0000u),
                   __uint_as_float(v.z & 0xFFFF0000u), __uint_as_float(v.w & 0xFFFF0000u));
@@ -783,10 +845,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
             }
           }
           if (!__any(pend)) break;
-          if (spin >= kSpinLimit) {
-            timed_out = true;
-            break;
-          }
+          if (give_up(wst, spin)) break;
           __builtin_amdgcn_s_sleep(1);
         }
       }
@@ -797,7 +856,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
                                         p.residual_mode, s_x[cur ^ 1][h], p.residual, h);
         store_xcd_u32(sc->xl[xcd][cur], H, h, tagged(ob, tag));
       }
-      poll_tagged<2, kXcdLoadAux>(sc->xl[xcd][cur], H, tag, s_x[cur], lane, wave, timed_out);
+      poll_tagged<2, kXcdLoadAux>(sc->xl[xcd][cur], H, tag, s_x[cur], lane, wave, wst);
     }
     __syncthreads();
     float* const s_xc = s_x[cur];
@@ -835,8 +894,9 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       GateRow<RQ> rw;
       gate_row_from_lds<RQ>(rw, s_rw[wave], lane);
       const float acc = wave_sum(gate_partial(rw, s_in, lane));
-      if (row < E && lane == 0)
-        store_xcd_u32(sc->logits[xcd], E, row, tagged(f32_to_bf16(acc), tag));
+      if (lane == 0)
+        store_xcd_u32(sc->logits[xcd], kFusedMaxExperts, row,
+                      tagged(row < E ? f32_to_bf16(acc) : 0u, tag));
     }
 
     // ---- S: the shared pair of waves 6 and 7 (stored after the routed
@@ -854,8 +914,8 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     uint32_t my = 0;
     if (wave == kPollWave) {
       const __amdgpu_buffer_rsrc_t rs = rsrc(sc->logits[xcd], E * 4);
-      uint32_t w[kPer];
-      for (int spin = 0;; ++spin) {
+      uint32_t w[kPer] = {0u, 0u, 0u, 0u};
+      for (int spin = 0; !wst.gave_up; ++spin) {
         bool ok = true;
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, 0, kXcdLoadAux);
         w[0] = v.x;
@@ -865,10 +925,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 #pragma unroll
         for (int i = 0; i < kPer; ++i) ok &= 4 * lane + i >= E || tag_ok(w[i], tag);
         if (__all(ok)) break;
-        if (spin >= kSpinLimit) {
-          timed_out = true;
-          break;
-        }
+        if (give_up(wst, spin)) break;
         __builtin_amdgcn_s_sleep(1);
       }
       uint32_t k[kPer];
@@ -936,6 +993,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         if (lane == 0) store_xcd_u32(sc->xact[xcd], I, vg + kXcdWaves * pp, tagged(a, tag));
         __builtin_amdgcn_sched_barrier(0);
       }
+    } else if (lane == 0) {
+      // an XCD without a routed slot in this call still tags its words
+#pragma unroll
+      for (int pp = 0; pp < kRoutedPairs; ++pp)
+        store_xcd_u32(sc->xact[xcd], I, vg + kXcdWaves * pp, tagged(0u, tag));
     }
 
     // The next layer's router rows: issued inside the routed stream rather
@@ -978,9 +1040,9 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
 
     // ---- collect the activations: routed (XCD-local) and shared.
     if (routed && (wave == 2 || wave == 3))
-      poll_tagged<1, kXcdLoadAux>(sc->xact[xcd], I, tag, s_act, lane, wave - 2, timed_out);
+      poll_tagged<1, kXcdLoadAux>(sc->xact[xcd], I, tag, s_act, lane, wave - 2, wst);
     if (wave == 4 || wave == 5)
-      poll_tagged<1, kSc1>(sc->sact[cur], I, tag, s_ash, lane, wave - 4, timed_out);
+      poll_tagged<1, kSc1>(sc->sact[cur], I, tag, s_ash, lane, wave - 4, wst);
     __syncthreads();
 
     // ---- D: eight routed down rows per wave, two shared rows per loader
@@ -995,23 +1057,26 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
           s_yo[wave * kXcdRows + i * (64 / kLanesPerRow) + lane / kLanesPerRow] =
               tagged(f32_to_bf16(y[i]), tag);
       }
+    } else if (lane < kXcdRows) {
+      s_yo[wave * kXcdRows + lane] = tagged(0u, tag);
     }
-    if (loader && has_shared) {
+    if (loader) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const float y = row_dot<BITS>(sdr[t], sdpw[t], s_ash, lane);
+        const float y = has_shared ? row_dot<BITS>(sdr[t], sdpw[t], s_ash, lane) : 0.0f;
         if (lane == 0) s_yo[kWaves * kXcdRows + 2 * q + t] = tagged(f32_to_bf16(y), tag);
       }
     }
     __syncthreads();
-    // ---- the workgroup's unit outputs, from one wave: 64 routed rows of
-    // this XCD's unit (16-byte stores, lanes 0-15) and 8 shared rows (16-17).
+    // ---- the workgroup's unit outputs, from one wave: 64 rows of this
+    // XCD's routed slot (16-byte stores, lanes 0-15; zeros when the call
+    // has no such slot) and 8 rows of the shared expert's slot (16-17).
     if (wave == kWaves - 1) {
-      const bool on = lane < 16 ? routed : (lane < 18 && has_shared);
-      if (on) {
+      if (lane < 18) {
         const uint4 v = *reinterpret_cast<const uint4*>(s_yo + 4 * lane);
         const int dst = lane < 16 ? xcd * H + j * (kWaves * kXcdRows) + 4 * lane
-                                  : K * H + xcd * kXcdWaves + j * kXcdRows + 4 * (lane - 16);
+                                  : kMaxFusedRouted * H + xcd * kXcdWaves + j * kXcdRows +
+                                        4 * (lane - 16);
         u32x4 w;
         w.x = v.x;
         w.y = v.y;
@@ -1027,21 +1092,19 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   {
     const int lane = lane0;
     const int last = p.n_layers - 1;
-    const uint32_t tag = base + 1 + last;
+    const uint32_t tag = phase_tag(base + 1 + last);
     const int h = wg * kWaves + wave;
     const __amdgpu_buffer_rsrc_t rs = rsrc(sc->ys[last & 1][0], NU * H * 4);
-    bool pend = lane < U;
+    bool pend = lane < U && !wst.gave_up;
+    const int slot = lane < K ? lane : kMaxFusedRouted;  // unit lane's slot
     uint32_t wv = 0;
     for (int spin = 0;; ++spin) {
       if (pend) {
-        wv = __builtin_amdgcn_raw_buffer_load_b32(rs, (lane * H + h) * 4, 0, kSc1);
+        wv = __builtin_amdgcn_raw_buffer_load_b32(rs, (slot * H + h) * 4, 0, kSc1);
         pend = !tag_ok(wv, tag);
       }
       if (!__any(pend)) break;
-      if (spin >= kSpinLimit) {
-        timed_out = true;
-        break;
-      }
+      if (give_up(wst, spin)) break;
       __builtin_amdgcn_s_sleep(1);
     }
     float y[NU];
@@ -1052,7 +1115,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       p.out[h] = (uint16_t)combine_row(y, 1, s_coef, K, has_shared, p.residual_mode,
                                        s_x[last & 1][h], p.residual, h);
   }
-  if (timed_out) store_coherent_u32(&sc->err, 1u);
   // Workgroup 0 has read every workgroup's shared activations of the last
   // layer, each written after that workgroup read the epoch.
   if (wg == 0 && threadIdx.x == 0) store_coherent_u32(&sc->epoch, base + p.n_layers);

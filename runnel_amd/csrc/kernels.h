@@ -81,12 +81,16 @@ struct FusedLayer {
 
 // Device scratch of the fused kernel: lives at a fixed workspace offset so
 // the epoch persists across calls of any shape.  Values handed between
-// workgroups are tagged words: (bf16 value << 16) | (phase & 0xFFFF).  Rows
-// indexed by XCD are written and read inside that XCD only (its L2).
+// workgroups are tagged words: (bf16 value << 16) | (phase % 65535 + 1).
+// Rows indexed by XCD are written and read inside that XCD only (its L2).
+// err is the status word (0 ok, 1 a wait gave up, 2 a workgroup did not run
+// on XCD i % 8); abort holds the first phase of a call in which a workgroup
+// gave up, so that the other workgroups of that call stop waiting.
 struct FusedScratch {
   uint32_t epoch;
   uint32_t err;
-  uint32_t pad[62];
+  uint32_t abort;
+  uint32_t pad[61];
   uint32_t logits[8][kFusedMaxExperts];       // router logits of XCD x
   uint32_t xact[8][kFusedI];                  // routed activations of XCD x
   uint32_t sact[2][kFusedI];                  // shared activations, by layer parity
@@ -165,7 +169,8 @@ struct PrefillArgs {
 // ---- the static scratch of rmoe_moe_block_noalloc (noalloc.hip).
 constexpr size_t kStaticScratchBytes = size_t(16) << 20;
 // Device address of this device's copy (looked up once per device).
-hipError_t static_scratch(void** out);
+// Device address of the static scratch on the device `stream` runs on.
+hipError_t static_scratch(hipStream_t stream, void** out);
 // *out = *word, then *word = 0 (one tiny kernel on `s`).
 hipError_t launch_take_status(uint32_t* word, uint32_t* out, hipStream_t s);
 

@@ -26,26 +26,36 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void* g_ptr[kMaxDevices];  // device address of `scratch`, per device
 
-// Copies the status word into the caller's output and clears it, so each
-// call reports its own outcome (the word is sticky otherwise).
+// Copies the status word into the caller's output (when given) and clears
+// it, so that each call reports its own outcome (the word is sticky
+// otherwise).
 __global__ void take_status_kernel(uint32_t* word, uint32_t* out) {
   if (threadIdx.x == 0) {
-    *out = *word;
+    if (out) *out = *word;
     *word = 0u;
   }
 }
 
 }  // namespace
 
-hipError_t static_scratch(void** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+hipError_t static_scratch(hipStream_t stream, void** out) {
+  // the copy of the device the stream runs on, resolved with that device
+  // current
+  int dev = 0, cur = 0;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_mu);
   if (!g_ptr[dev]) {
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
     if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
     g_ptr[dev] = p;

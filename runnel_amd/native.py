@@ -300,13 +300,14 @@ def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None
               workspace: torch.Tensor | None = None, check: bool | None = None):
     """Whole SparseMoeBlock on x bf16 [T, H] -> bf16 [T, H].
 
-    ``check``: read (and clear) the workspace's status word after the call
-    and raise RmoeError(RMOE_ETIMEOUT) if a cross-workgroup wait of the
-    single-launch decode gave up; this synchronises the stream.  None (the
-    default) checks one-token calls made with plain launches
-    (``set_cooperative_launch(False)``) outside graph capture, the only
-    eager calls whose waits can give up; graph users call ``check_status``
-    on the workspace after a replay."""
+    ``check``: True reads (and clears) the workspace's status word after the
+    call and raises RmoeError (RMOE_ETIMEOUT / RMOE_EPLACEMENT) if the
+    single-launch decode failed; this synchronises the stream.  None (the
+    default) checks eager one-token calls without waiting for the device:
+    behind the first call on a workspace and every 32nd after it, the word
+    is copied to pinned host memory, and a later eager call on the
+    workspace examines the copy once it has landed and raises then.  False skips the check; graph
+    users call ``check_status`` on the workspace after a replay."""
     lib = _lib.load()
     H = layer.hidden
     _check_x(x, H)
@@ -327,14 +328,17 @@ def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None
         scores = torch.empty((T, layer.top_k), dtype=torch.float32, device=x.device)
     need = layer.workspace_bytes(T)
     ws = workspace if workspace is not None else WORKSPACE.get(x.device, need, "block")
-    if check is None:
-        check = T == 1 and not _COOPERATIVE[0] and not _capturing(x.device)
+    deferred = check is None and T == 1 and not _capturing(x.device)
+    if deferred:
+        _STATUS.poll(ws)
     _lib.check(lib.rmoe_moe_block(ctypes.byref(layer.struct), x.data_ptr(), T,
                                   _lib.ptr(residual), out.data_ptr(), _lib.ptr(idx),
                                   _lib.ptr(scores), ws.data_ptr(), ws.numel(),
                                   _lib.stream_handle(x.device)))
     if check:
         check_status(ws)
+    elif deferred:
+        _STATUS.after_call(ws)
     if return_routing:
         return out, idx, scores
     return out
@@ -365,7 +369,8 @@ def moe_chain(chain: Chain, x: torch.Tensor, out: torch.Tensor | None = None,
               workspace: torch.Tensor | None = None,
               check: bool | None = None) -> torch.Tensor:
     """One token x bf16 [1, H] (or [H]) through every layer of the chain.
-    ``check`` as for ``moe_block`` (None: check plain eager launches)."""
+    ``check`` as for ``moe_block`` (None: the deferred check of eager
+    calls)."""
     lib = _lib.load()
     H = chain.layers[0].hidden
     if x.dtype != BF16 or x.numel() != H or x.dim() not in (1, 2):
@@ -379,19 +384,22 @@ def moe_chain(chain: Chain, x: torch.Tensor, out: torch.Tensor | None = None,
         out = torch.empty_like(x)
     ws = workspace if workspace is not None else WORKSPACE.get(
         x.device, chain.workspace_bytes(), "block")
-    if check is None:
-        check = not _COOPERATIVE[0] and not _capturing(x.device)
+    deferred = check is None and not _capturing(x.device)
+    if deferred:
+        _STATUS.poll(ws)
     _lib.check(lib.rmoe_moe_chain(ctypes.byref(chain.layers[0].struct), chain.table.data_ptr(),
                                   chain.n, x.data_ptr(), out.data_ptr(), ws.data_ptr(),
                                   ws.numel(), _lib.stream_handle(x.device)))
     if check:
         check_status(ws)
+    elif deferred:
+        _STATUS.after_call(ws)
     return out
 
 
 # The launch mode last set through set_cooperative_launch (the library's
-# default is cooperative).
-_COOPERATIVE = [True]
+# default is a plain launch).
+_COOPERATIVE = [False]
 
 
 def _capturing(device) -> bool:
@@ -400,21 +408,25 @@ def _capturing(device) -> bool:
 
 def set_cooperative_launch(enabled: bool) -> bool:
     """Launch mode of the single-launch decode kernel outside graph capture
-    (process-wide; returns the previous mode).  False: plain launches, which
-    overlap the previous call (about 17 us less per eager call) and are
-    valid while nothing else runs on the device during the call; moe_block
-    and moe_chain then check the status word after each one-token call
-    unless told not to."""
+    (process-wide; returns the previous mode).  False (the library's
+    default): plain launches, as a captured graph makes them (about 14 us
+    per eager one-token call back to back).  True: cooperative launches,
+    which guarantee that every workgroup is resident whatever runs on other
+    streams, at about 18 us more per call (two plain single-launch calls
+    overlapping on different streams can hold each other's CUs; their
+    waits then give up and set the status word, which the deferred check
+    of eager calls reports)."""
     prev = bool(_lib.load().rmoe_set_cooperative_launch(1 if enabled else 0))
     _COOPERATIVE[0] = bool(enabled)
     return prev
 
 
 def workspace_status(ws: torch.Tensor, clear: bool = False) -> int:
-    """The status word of a workspace (nonzero: a single-launch decode timed
-    out waiting for another workgroup, and that call's outputs are not
-    valid).  The word is sticky: every later call leaves it set until it is
-    cleared.  Reading it synchronises with the work queued on ws's device."""
+    """The status word of a workspace: 0, or (the call's outputs are not
+    valid) 1 when a single-launch decode gave up a cross-workgroup wait or
+    was cancelled, 2 when a workgroup read an XCC id outside 0-7.  The word
+    is sticky: every later call leaves it set until it is cleared.  Reading
+    it synchronises with the work queued on ws's device."""
     off = _lib.load().rmoe_workspace_status_offset()
     word = ws[off:off + 4].view(torch.int32)
     v = int(word.item())
@@ -423,13 +435,70 @@ def workspace_status(ws: torch.Tensor, clear: bool = False) -> int:
     return v
 
 
+def _raise_status(v: int) -> None:
+    if v == 2:
+        raise _lib.RmoeError(_lib.RMOE_EPLACEMENT,
+                             "a single-launch decode read an XCC id outside 0-7; "
+                             "its outputs are not valid")
+    raise _lib.RmoeError(_lib.RMOE_ETIMEOUT,
+                         "a single-launch decode timed out waiting for another "
+                         "workgroup; its outputs are not valid")
+
+
 def check_status(ws: torch.Tensor) -> None:
-    """Raise RmoeError(RMOE_ETIMEOUT) if the workspace's status word is set,
-    clearing it first (graph users call this after a replay)."""
-    if workspace_status(ws, clear=True):
-        raise _lib.RmoeError(_lib.RMOE_ETIMEOUT,
-                             "a single-launch decode timed out waiting for another "
-                             "workgroup; its outputs are not valid")
+    """Raise RmoeError (RMOE_ETIMEOUT, RMOE_EPLACEMENT) if the workspace's
+    status word is set, clearing it first (graph users call this after a
+    replay)."""
+    _STATUS.forget(ws)
+    v = workspace_status(ws, clear=True)
+    if v:
+        _raise_status(v)
+
+
+class _StatusWatch:
+    """The deferred check of eager single-launch calls.  Behind the first
+    call on a workspace and then every `every`-th one, the status word is
+    copied (4 bytes) into pinned host memory and an event recorded; the
+    copy is read once that event has completed, at a later eager call on
+    the workspace, so the host never waits for the device.  The word is
+    sticky, so a copy also shows a failure of any call before it.  (A copy
+    behind every call costs about 11 us of host time per call.)"""
+
+    def __init__(self, every: int = 32):
+        self.every = every
+        self._ent: dict = {}
+
+    def after_call(self, ws: torch.Tensor) -> None:
+        key = (ws.device, ws.data_ptr())
+        ent = self._ent.get(key)
+        if ent is None:
+            ent = [torch.zeros(1, dtype=torch.int32, pin_memory=True),
+                   torch.cuda.Event(), False, 0]
+            self._ent[key] = ent
+        ent[3] += 1
+        if ent[2] or (ent[3] - 1) % self.every:
+            return
+        off = _lib.load().rmoe_workspace_status_offset()
+        ent[0].copy_(ws[off:off + 4].view(torch.int32), non_blocking=True)
+        ent[1].record()
+        ent[2] = True
+
+    def poll(self, ws: torch.Tensor) -> None:
+        ent = self._ent.get((ws.device, ws.data_ptr()))
+        if ent is None or not ent[2] or not ent[1].query():
+            return
+        ent[2] = False
+        if int(ent[0][0]):
+            check_status(ws)
+
+    def forget(self, ws: torch.Tensor) -> None:
+        ent = self._ent.get((ws.device, ws.data_ptr()))
+        if ent is not None:
+            ent[2] = False
+            ent[3] = 0
+
+
+_STATUS = _StatusWatch()
 
 
 def default_workspace(device, key: str = "block") -> torch.Tensor | None:

@@ -407,11 +407,12 @@ def test_bench_byte_model_matches_the_survey_figures():
 
 def test_cooperative_launch_switch_returns_previous_mode():
     """rmoe_set_cooperative_launch is process-wide and returns the previous
-    mode; cooperative launches are the default."""
+    mode; plain launches are the default."""
     lib = _lib.load()
+    assert lib.rmoe_set_cooperative_launch(1) == 0
     assert lib.rmoe_set_cooperative_launch(0) == 1
     assert lib.rmoe_set_cooperative_launch(7) == 0   # any nonzero turns it on
-    assert lib.rmoe_set_cooperative_launch(1) == 1
+    assert lib.rmoe_set_cooperative_launch(0) == 1
 
 
 def test_single_launch_shape_rejects_nine_routed_slots():

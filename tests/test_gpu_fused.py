@@ -224,14 +224,14 @@ def test_plain_eager_launch_equals_cooperative(torch_cuda):
     h = lw.handle()
     xs = synthetic.make_x(7301, 8, 2048)
     ws = torch.zeros(h.workspace_bytes(1), dtype=torch.uint8, device="cuda")
-    coop = [native.moe_block(h, xs[t:t + 1], workspace=ws) for t in range(8)]
-    prev = native.set_cooperative_launch(False)
+    prev = native.set_cooperative_launch(True)
     try:
-        assert prev is True
+        coop = [native.moe_block(h, xs[t:t + 1], workspace=ws) for t in range(8)]
+        assert native.set_cooperative_launch(False) is True
         plain = [native.moe_block(h, xs[t:t + 1], workspace=ws) for t in range(8)]
         torch.cuda.synchronize()
     finally:
-        native.set_cooperative_launch(True)
+        native.set_cooperative_launch(prev)
     assert native.workspace_status(ws) == 0
     for a, b in zip(coop, plain):
         assert torch.equal(a, b)
