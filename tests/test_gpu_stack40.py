@@ -2,7 +2,9 @@
 (hidden 2048, 256 experts, top-8 + shared, inter 512; the same seeds and
 first input as bench.py) chained through all 40 layers in one launch, and
 every layer checked against the oracle, as the reference checks each of the
-40 layers of its real-tensor sweep (bench/run_native_ornith_layers.py:41-111).
+40 layers of its real-tensor sweep (bench/run_native_ornith_layers.py:41-111),
+and the whole chain against the oracle's own 40-layer chain run with the
+GPU's routing.
 
 The chained kernel's output after l layers comes from a chain of the first
 l layers (the same kernel and arithmetic), so each layer's input and output
@@ -11,12 +13,20 @@ are known; the oracle copies one layer to the host at a time."""
 import numpy as np
 import pytest
 
-from helpers import cosine, host_bf16, layer_from_dev
+from helpers import host_bf16, layer_from_dev
 from oracle import moe_ref as M
 
 pytestmark = pytest.mark.gpu
 
 N_LAYERS = 40
+# The end-to-end bar: the GPU chain and the oracle's chain (the GPU's routing
+# forced) may differ, element by element, by E2E_FACTOR times the sum of the
+# per-layer rounding allowances.  Each layer adds new rounding differences
+# within its allowance; the residual stream carries earlier ones with gain
+# one, and the block adds their image through its Jacobian, which grows with
+# |x| along the chain: on this workload the ratio stays under 0.45 through
+# layer 30 and reaches 1.8 at layer 39 (x grows to several units).
+E2E_FACTOR = 4.0
 
 
 @pytest.fixture(scope="module")
@@ -86,13 +96,16 @@ def test_forty_layer_chain_matches_the_oracle_at_every_layer(torch_cuda):
     assert native.workspace_status(ws) == 0
     assert torch.equal(full, ys[N_LAYERS])
     print("chain done; checking every layer", flush=True)
-    # The oracle also runs the chain on its own inputs.  Routing is
-    # discontinuous: once rounding differences move a later layer's k-th and
-    # (k+1)-th logits past each other the two chains use different experts,
-    # so they are compared end to end only up to that layer; every layer is
-    # held to the tight bar on the GPU's own input regardless.
+    # The oracle also runs the chain end to end on its own inputs, with the
+    # GPU's routing forced at every layer (routing is discontinuous: without
+    # that, rounding differences that move a later layer's k-th and
+    # (k+1)-th logits past each other would send the two chains to
+    # different experts).  The two chains' difference at layer l is held,
+    # element by element, to E2E_FACTOR times the sum of the rounding
+    # allowances of the layers up to it.
     cur_ref = host_bf16(x)
-    split_at = None
+    sum_allow = np.zeros(2048)
+    worst = 0.0
     for l in range(N_LAYERS):
         L = layer_from_dev(stack[l])
         xin = host_bf16(ys[l])
@@ -102,7 +115,8 @@ def test_forty_layer_chain_matches_the_oracle_at_every_layer(torch_cuda):
         torch.cuda.synchronize()
         # the single-layer call of the same kernel agrees with the chain
         assert torch.equal(one, ys[l + 1]), f"layer {l}"
-        assert np.array_equal(idx.cpu().numpy(), ref_idx), f"layer {l}"
+        gidx = idx.cpu().numpy()
+        assert np.array_equal(gidx, ref_idx), f"layer {l}"
         got = host_bf16(ys[l + 1])
         # every element within 2^-6 of the contract plus the steps of its
         # rounded intermediates (a different fp32 order flips a rounding
@@ -110,26 +124,18 @@ def test_forty_layer_chain_matches_the_oracle_at_every_layer(torch_cuda):
         # the result)
         allow = _rounding_allowance(L, xin, ref_idx, ref_scores)
         assert _contract_mismatches(got, ref, allow) == 0, f"layer {l}"
-        if split_at is None:
-            nxt, own_idx, _ = M.block_forward(L, cur_ref, residual_bits=cur_ref)
-            if not np.array_equal(np.sort(own_idx, -1), np.sort(ref_idx, -1)):
-                split_at = l
-                lg = M.round_bf16(M.gate_logits(cur_ref, L.router_w))[0]
-                srt = np.sort(lg)[::-1]
-                print(f"the oracle's own chain routes differently from layer {l} on "
-                      f"(its 8th / 9th logits {srt[7]:.5f} / {srt[8]:.5f})", flush=True)
-                assert l > 0   # the first layer sees the same input
-            else:
-                cur_ref = nxt
-                # rounding differences compound through the residual stream
-                # (which grows to several units, where one bf16 step exceeds
-                # 2e-2): the two chains are held to norm-wise bounds
-                g = M.bf16_to_f32(got).astype(np.float64)
-                r = M.bf16_to_f32(cur_ref).astype(np.float64)
-                assert np.linalg.norm(g - r) <= 1e-2 * np.linalg.norm(r), f"layer {l}"
-                assert cosine(g, r) >= 0.9999, f"layer {l}"
-        del L
+        # end to end
+        nxt, _, sc = M.block_forward(L, cur_ref, residual_bits=cur_ref, idx=gidx)
+        sum_allow += _rounding_allowance(L, cur_ref, gidx, sc)
+        cur_ref = nxt
+        e = np.abs(M.bf16_to_f32(got).astype(np.float64) -
+                   M.bf16_to_f32(cur_ref).astype(np.float64))
+        ratio = float((e / sum_allow).max())
+        worst = max(worst, ratio)
         if l % 10 == 9:
-            print(f"layers 0..{l} ok", flush=True)
-    print(f"end-to-end agreement over {split_at if split_at is not None else N_LAYERS} "
-          "layers", flush=True)
+            print(f"layers 0..{l} ok; end-to-end max |diff| {e.max():.4g}, largest "
+                  f"ratio to the allowance sum {ratio:.3g}", flush=True)
+        assert (e <= E2E_FACTOR * sum_allow).all(), f"layer {l}: ratio {ratio:.3g}"
+        del L
+    print(f"end-to-end: largest ratio to the allowance sum {worst:.3g}", flush=True)
+
