@@ -308,7 +308,7 @@ def run_decode_single(torch, bits, copies=16, calls=64, reps=20, warmup=3, seed0
     }
 
 
-def run_few_tokens(torch, stack, tokens, steps=20, warmup=3, seed=11):
+def run_few_tokens(torch, stack, tokens, steps=20, warmup=3, seed=11, bits=8):
     """A few tokens through every layer of the stack, one block call per
     layer (router, gate/up and down launches: the few-token kernels), each
     layer's output plus residual feeding the next.  The passes over the
@@ -330,8 +330,8 @@ def run_few_tokens(torch, stack, tokens, steps=20, warmup=3, seed=11):
         a, b = bufs[l & 1], bufs[(l + 1) & 1]
         _, idx, _ = native.moe_block(h, a, residual=a, out=b, workspace=ws, return_routing=True)
         distinct.append(len(np.unique(idx.cpu().numpy())))
-    per_expert = layer_bytes(H, 512, 256, 1, 8, shared=False, tokens=0) - 256 * H * 2
-    fixed = layer_bytes(H, 512, 256, 0, 8, shared=True, tokens=tokens, residual=True)
+    per_expert = layer_bytes(H, 512, 256, 1, bits, shared=False, tokens=0) - 256 * H * 2
+    fixed = layer_bytes(H, 512, 256, 0, bits, shared=True, tokens=tokens, residual=True)
     pass_bytes = sum(d * per_expert + fixed for d in distinct)
 
     def one_pass():
@@ -438,11 +438,13 @@ def main():
                     help="replay captured HIP graphs (default), launch eagerly every "
                          "step (plain launches, the library's default), or eagerly "
                          "with cooperative launches (rmoe_set_cooperative_launch(1))")
-    ap.add_argument("--workload", choices=["decode40", "prefill512", "prefill8192", "few"],
+    ap.add_argument("--workload",
+                    choices=["decode40", "decode1", "prefill512", "prefill8192", "few"],
                     default="decode40",
-                    help="decode40: the bench line; the prefill workloads and few "
-                         "(2, 4 and 7 tokens through the 40-layer stack) print their "
-                         "own line (exploration and profiling)")
+                    help="decode40: the bench line; decode1 (one layer per call, "
+                         "--bits), the prefill workloads and few (2, 4 and 7 tokens "
+                         "through the 40-layer stack) print their own line "
+                         "(exploration and profiling)")
     ap.add_argument("--few-tokens", default="2,4,7",
                     help="token counts of --workload few (comma-separated)")
     ap.add_argument("--no-prefill", action="store_true",
@@ -466,11 +468,15 @@ def main():
     if args.calibrate_copy:
         return calibrate_copy(torch)
     if args.workload == "few":
-        stack = build_stack(args.layers, 8)
+        stack = build_stack(args.layers, args.bits)
         torch.cuda.synchronize()
-        print(json.dumps({"workload": "few", "runs": [
-            run_few_tokens(torch, stack, int(T), args.steps, args.warmup)
+        print(json.dumps({"workload": "few", "bits": args.bits, "runs": [
+            run_few_tokens(torch, stack, int(T), args.steps, args.warmup, bits=args.bits)
             for T in args.few_tokens.split(",")]}), flush=True)
+        return 0
+    if args.workload == "decode1":
+        print(json.dumps({"workload": "decode1",
+                          **run_decode_single(torch, args.bits, reps=args.steps)}), flush=True)
         return 0
     if args.workload != "decode40":
         tokens, bits, skewed = (512, 8, False) if args.workload == "prefill512" else (8192, 4, True)
@@ -549,6 +555,7 @@ def main():
                 "bytes_per_launch": b4, "us_per_launch": round(r4["us_token"], 3),
             },
         }
+        out["few_token_4bit"] = run_few_tokens(torch, r4["stack"], 4, bits=4)
         del r4
         # one layer per call at 8 and 4 bits, rotating over 16 copies
         out["decode_1layer_8bit"] = run_decode_single(torch, 8)

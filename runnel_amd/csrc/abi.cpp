@@ -362,15 +362,15 @@ bool fused_eligible(const rmoe_layer* L, int* grid) {
 }
 
 // The few-token decode kernels (decode.hip): 2..kFewMaxTokens tokens below
-// the expert-sorted path, at the single-launch shapes with 8-bit experts;
-// their gate/up reads each row's scales and biases as 4-byte words.
+// the expert-sorted path, at the single-launch shapes with 8- or 4-bit
+// experts; their gate/up reads each row's scales and biases as 4-byte words.
 bool few_eligible(const rmoe_layer* L, int T, bool sorted) {
   auto words = [](const rmoe_qweight& q) {
     return aligned(q.scales, 4) && aligned(q.biases, 4);
   };
   const bool shared = L->shared_gate_up.w != nullptr;
   return T >= 2 && T <= rmoe::kFewMaxTokens && !sorted && fused_shape_ok(L) &&
-         L->gate_up.bits == 8 && words(L->gate_up) && (!shared || words(L->shared_gate_up));
+         words(L->gate_up) && (!shared || words(L->shared_gate_up));
 }
 
 rmoe::FusedLayer fused_layer(const rmoe_layer* L) {
@@ -698,7 +698,7 @@ int block_launch(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   a.residual = residual;
   a.idx_out = indices_out;
   a.scores_out = scores_out;
-  if (few_eligible(L, tokens, lay.rows != 0)) a.few_bits = 8;
+  if (few_eligible(L, tokens, lay.rows != 0)) a.few_bits = L->gate_up.bits;
   if (lay.rows && rmoe::router_mfma_eligible(L->experts, L->hidden))
     e = rmoe::launch_router_mfma(
         a, reinterpret_cast<float*>(static_cast<char*>(ws) + lay.wnorm),

@@ -1298,26 +1298,38 @@ __device__ __forceinline__ uint32_t codes_bf16x2(uint32_t w, int pair) {
   const float f1 = (float)((w >> (16 * pair + 8)) & 0xFFu);
   return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
 }
+// The same for 4-bit codes 2 j and 2 j + 1 of a word, from its even nibbles
+// (lo = w & 0x0F0F0F0F: codes 0, 2, 4, 6 as bytes) and odd ones (hi).
+__device__ __forceinline__ uint32_t nibbles_bf16x2(uint32_t lo, uint32_t hi, int j) {
+  const float f0 = (float)((lo >> (8 * j)) & 0xFFu);
+  const float f1 = (float)((hi >> (8 * j)) & 0xFFu);
+  return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
 
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// One wave per kDownRows output rows of one token, all its units: lane
-// (r, ch) holds 16-byte chunk ch (16 codes) of rows h0 + 2 rp + r, and the
-// token's bf16 activations of that chunk (an L2 hit), unit by unit in a
-// window of kWindow units.  Codes become bf16 pairs for v_dot2_f32_bf16
-// against the packed activations.  COMBINE: weighted sum in slot order,
-// gated shared expert, residual; otherwise per-slot rows y[t, j, h].
-template <bool COMBINE>
-__global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
+// One wave per kDownRows output rows of one token, all its units.  8-bit:
+// lane (r, ch) holds 16-byte chunk ch (16 codes) of rows h0 + 2 rp + r (32
+// lanes a row, RP = 2 row pairs); 4-bit: chunk ch (32 codes) of row h0 + r
+// (16 lanes a row, r < 4, one pass).  With the chunk, the token's bf16
+// activations of it (an L2 hit), unit by unit in a window of kWindow units.
+// Codes become bf16 pairs for v_dot2_f32_bf16 against the packed
+// activations.  COMBINE: weighted sum in slot order, gated shared expert,
+// residual; otherwise per-slot rows y[t, j, h].
+template <int BITS, bool COMBINE>
+__global__ __launch_bounds__(256) void down_few_kernel(const DecodeArgs p) {
   constexpr int H = few::H;
   constexpr int I = few::I;
   constexpr int NU = kMaxFusedUnits;
   constexpr int D = few::kWindow;
-  constexpr int RP = few::kDownRowPairs;
-  constexpr int WPR = I / 4;  // words per down row
+  constexpr int LPR = BITS == 8 ? 32 : 16;          // lanes per row
+  constexpr int RPW = 64 / LPR;                      // rows per pass: 2 | 4
+  constexpr int RP = few::kDownRows / RPW;           // passes: 2 | 1
+  constexpr int VPL = BITS == 8 ? 16 : 32;           // values per lane
+  constexpr int WPR = I * BITS / 32;  // words per down row
   constexpr int GD = I / 64;  // groups per down row
   const int K = p.K;
   const int U1 = K + p.has_shared;
@@ -1328,9 +1340,10 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
   const int t = gw / few::kDownWavesPerToken;
   if (t >= p.T) return;
   const int h0 = (gw - t * few::kDownWavesPerToken) * few::kDownRows;
-  const int r = lane >> 5;
-  const int ch = lane & 31;
-  const uint16_t* act = reinterpret_cast<const uint16_t*>(p.act) + (size_t)t * U1 * I + ch * 16;
+  const int r = lane / LPR;
+  const int ch = lane & (LPR - 1);
+  const uint16_t* act =
+      reinterpret_cast<const uint16_t*>(p.act) + (size_t)t * U1 * I + ch * VPL;
 
   // Experts of the token's slots; an index outside the bank (a caller's)
   // reads expert 0 and contributes zero.  Loads are issued without branches
@@ -1369,19 +1382,20 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
 #pragma unroll
   for (int u = 0; u < NU; ++u)
     score[u] = (COMBINE && u < units) ? p.scores[t * p.score_stride + u] : 0.0f;
-  uint4 av[NU][2];
+  constexpr int AV = VPL / 8;  // 16-byte activation pieces per lane
+  uint4 av[NU][AV];
   uint4 wv[NU][RP];
   uint32_t sv[NU][RP], bv[NU][RP];
   auto issue = [&](int u) {
-    av[u][0] = load16(act + ua[u] * I);
-    av[u][1] = load16(act + ua[u] * I + 8);
+#pragma unroll
+    for (int i = 0; i < AV; ++i) av[u][i] = load16(act + ua[u] * I + 8 * i);
     const QW& q = ush[u] ? sdn : dn;
 #pragma unroll
     for (int rp = 0; rp < RP; ++rp) {
-      const size_t row = (size_t)ev[u] * H + h0 + 2 * rp + r;
+      const size_t row = (size_t)ev[u] * H + h0 + RPW * rp + r;
       wv[u][rp] = load16_stream(q.w + row * WPR + ch * 4);
-      sv[u][rp] = q.s[row * GD + (ch >> 2)];
-      bv[u][rp] = q.b[row * GD + (ch >> 2)];
+      sv[u][rp] = q.s[row * GD + (ch * VPL >> 6)];
+      bv[u][rp] = q.b[row * GD + (ch * VPL >> 6)];
     }
   };
 #pragma unroll
@@ -1394,31 +1408,43 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
     if (u + D < NU) issue(u + D);
     issue_fence();
     if (u < units) {  // wave-uniform
-      const uint32_t aw[8] = {av[u][0].x, av[u][0].y, av[u][0].z, av[u][0].w,
-                              av[u][1].x, av[u][1].y, av[u][1].z, av[u][1].w};
+      uint32_t aw[VPL / 2];
+#pragma unroll
+      for (int i = 0; i < AV; ++i) {
+        aw[4 * i] = av[u][i].x;
+        aw[4 * i + 1] = av[u][i].y;
+        aw[4 * i + 2] = av[u][i].z;
+        aw[4 * i + 3] = av[u][i].w;
+      }
       float asum = 0.0f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
+      for (int k = 0; k < VPL / 2; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
 #pragma unroll
       for (int rp = 0; rp < RP; ++rp) {
         const uint32_t ww[4] = {wv[u][rp].x, wv[u][rp].y, wv[u][rp].z, wv[u][rp].w};
         float dot = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          dot = dot2_bf16(codes_bf16x2(ww[k], 0), aw[2 * k], dot);
-          dot = dot2_bf16(codes_bf16x2(ww[k], 1), aw[2 * k + 1], dot);
+          if constexpr (BITS == 8) {
+            dot = dot2_bf16(codes_bf16x2(ww[k], 0), aw[2 * k], dot);
+            dot = dot2_bf16(codes_bf16x2(ww[k], 1), aw[2 * k + 1], dot);
+          } else {
+            const uint32_t lo = ww[k] & 0x0F0F0F0Fu, hi = (ww[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dot = dot2_bf16(nibbles_bf16x2(lo, hi, j), aw[4 * k + j], dot);
+          }
         }
         // converted here, not where they are loaded (which waited for them)
         uint32_t sw = sv[u][rp], bw = bv[u][rp];
         asm volatile("" : "+v"(sw), "+v"(bw));
         float y = bf16_to_f32(sw) * dot + bf16_to_f32(bw) * asum;
-        y = round_bf16(segment_sum_fast(y, 32));
+        y = round_bf16(segment_sum_fast(y, LPR));
         y = (bad >> u) & 1u ? 0.0f : y;
         if constexpr (COMBINE) {
           acc[rp] += score[u] * y;
         } else {
           if (ch == 0)
-            p.out[((size_t)t * K + u) * H + h0 + 2 * rp + r] = (uint16_t)f32_to_bf16(y);
+            p.out[((size_t)t * K + u) * H + h0 + RPW * rp + r] = (uint16_t)f32_to_bf16(y);
         }
       }
     }
@@ -1428,7 +1454,7 @@ __global__ __launch_bounds__(256) void down_few8_kernel(const DecodeArgs p) {
     if (ch == 0) {
 #pragma unroll
       for (int rp = 0; rp < RP; ++rp) {
-        const int h = h0 + 2 * rp + r;
+        const int h = h0 + RPW * rp + r;
         float o = round_bf16(acc[rp]);
         if (p.residual) o = round_bf16(bf16_to_f32(p.residual[(size_t)t * H + h]) + o);
         p.out[(size_t)t * H + h] = (uint16_t)f32_to_bf16(o);
@@ -1568,10 +1594,13 @@ template <int TB>
 static void router_tb(const DecodeArgs& a, hipStream_t s) {
   const int rows = a.E + a.has_sg;
   dim3 grid((rows + 3) / 4, (a.T + TB - 1) / TB);
-  if (a.few_bits == 8 && a.has_shared) {
+  if (a.few_bits != 0 && a.has_shared) {
     // plus the shared expert's gate/up (E <= 256 on the few-token path)
     grid.x += few::kSharedBlocks;
-    hipLaunchKernelGGL((router_kernel<4, TB, 8>), grid, dim3(256), 0, s, a);
+    if (a.few_bits == 8)
+      hipLaunchKernelGGL((router_kernel<4, TB, 8>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((router_kernel<4, TB, 4>), grid, dim3(256), 0, s, a);
   } else if (a.E <= 256) {
     hipLaunchKernelGGL((router_kernel<4, TB, 0>), grid, dim3(256), 0, s, a);
   } else {
@@ -1604,10 +1633,13 @@ static hipError_t gate_up_cpl(const DecodeArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s) {
-  if (a.few_bits == 8) {
+  if (a.few_bits != 0) {
     const int waves = a.T * a.K * few::kWavesPerUnit;
-    hipLaunchKernelGGL(gate_up_few_kernel<8>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
-                       s, a);
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (a.few_bits == 8)
+      hipLaunchKernelGGL(gate_up_few_kernel<8>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(gate_up_few_kernel<4>, grid, dim3(256), 0, s, a);
     RMOE_CHECK_LAUNCH();
     return hipSuccess;
   }
@@ -1624,12 +1656,19 @@ hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s) {
 }
 
 hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s) {
-  if (a.few_bits == 8) {
+  if (a.few_bits != 0) {
     const dim3 grid((unsigned)(a.T * few::kDownWavesPerToken / 4));
-    if (combine)
-      hipLaunchKernelGGL(down_few8_kernel<true>, grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(down_few8_kernel<false>, grid, dim3(256), 0, s, a);
+    if (a.few_bits == 8) {
+      if (combine)
+        hipLaunchKernelGGL((down_few_kernel<8, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((down_few_kernel<8, false>), grid, dim3(256), 0, s, a);
+    } else {
+      if (combine)
+        hipLaunchKernelGGL((down_few_kernel<4, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((down_few_kernel<4, false>), grid, dim3(256), 0, s, a);
+    }
     RMOE_CHECK_LAUNCH();
     return hipSuccess;
   }

@@ -40,8 +40,9 @@ struct DecodeArgs {
   int score_stride;  // K + 1 (the router's scores) or K (caller weights)
   float* act;        // [T, K + has_shared, I]
   uint32_t* ctr;     // [T] zero between calls
-  int few_bits;      // 8: the few-token kernels (act is bf16; the router
-                     // launch also computes the shared expert's gate/up)
+  int few_bits;      // 8 | 4: the few-token kernels at these bits (act is
+                     // bf16; the router launch also computes the shared
+                     // expert's gate/up); 0: the general kernels
   uint16_t* out;     // [T, H] (block) or [T, K, H] (switch)
   const uint16_t* residual;
   int32_t* idx_out;

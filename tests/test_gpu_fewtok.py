@@ -1,5 +1,5 @@
 """GPU parity of the few-token decode kernels (2..8 tokens below the
-expert-sorted threshold, hidden 2048, intermediate 512, 8-bit experts)
+expert-sorted threshold, hidden 2048, intermediate 512, 8- and 4-bit experts)
 against the oracle: the router launch that also runs the shared expert's
 gate/up, the gate/up kernel whose units share the rows of a repeated expert,
 and the down kernel's bf16-pair dot products.
@@ -51,11 +51,13 @@ def _check(got_bits, ref_bits, mlx_bits):
     dict(T=8, experts=32, top_k=4, shared=False, residual=False),
 ], ids=lambda c: f"T{c['T']}-E{c['experts']}-k{c['top_k']}"
                  f"{'-sh' if c['shared'] else ''}{'-res' if c['residual'] else ''}")
-def test_few_token_block(torch_cuda, case):
+@pytest.mark.parametrize("bits", [8, 4])
+def test_few_token_block(torch_cuda, case, bits):
     torch = torch_cuda
     from runnel_amd import native
-    L = M.make_layer(300 + case["T"] + case["experts"], hidden=2048, inter=512,
-                     experts=case["experts"], top_k=case["top_k"], bits=8,
+    print(f"few-token block bits={bits} {case}", flush=True)
+    L = M.make_layer(300 + case["T"] + case["experts"] + bits, hidden=2048, inter=512,
+                     experts=case["experts"], top_k=case["top_k"], bits=bits,
                      shared=case["shared"])
     x = M.make_x(40 + case["T"], case["T"], 2048)
     res = M.make_x(90 + case["T"], case["T"], 2048) if case["residual"] else None
@@ -73,13 +75,14 @@ def test_few_token_block(torch_cuda, case):
         assert len(np.unique(flat)) < flat.size
 
 
-def test_few_token_calls_repeat_bit_exact(torch_cuda):
+@pytest.mark.parametrize("bits", [8, 4])
+def test_few_token_calls_repeat_bit_exact(torch_cuda, bits):
     """The same call twice gives the same bits (no state carried between
     calls in the workspace), and a 1-token call in between does not disturb
     it."""
     torch = torch_cuda
     from runnel_amd import native
-    L = M.make_layer(77, hidden=2048, inter=512, experts=64, top_k=8, bits=8)
+    L = M.make_layer(77 + bits, hidden=2048, inter=512, experts=64, top_k=8, bits=bits)
     h = layer_to_dev(L)
     x4 = dev_bf16(M.make_x(3, 4, 2048))
     x1 = dev_bf16(M.make_x(4, 1, 2048))
