@@ -5,6 +5,9 @@ scores are equal bit for bit.  Two calls in a row on the shared static
 scratch, the second with a smaller input, on each path the block takes."""
 
 import ctypes
+import subprocess
+import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -90,3 +93,16 @@ def test_noalloc_small_layer_few_tokens(torch_cuda):
         _same(torch, a, _with_workspace(torch, h, x))
         _, ref_idx, _ = M.block_forward(L, xn)
         assert np.array_equal(a[1].cpu().numpy(), ref_idx)
+
+
+def test_noalloc_first_calls_under_graph_capture(torch_cuda):
+    """In a fresh process, the first noalloc calls (1 and 40 tokens) are made
+    under graph capture; replays equal the workspace path bit for bit with
+    status 0 (tests/noalloc_capture_case.py)."""
+    case = Path(__file__).resolve().parent / "noalloc_capture_case.py"
+    print("noalloc first calls under capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-u", str(case)], capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    assert "noalloc capture ok" in r.stdout
