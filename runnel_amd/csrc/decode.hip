@@ -36,9 +36,7 @@ constexpr int NP = 2;
 constexpr int kWavesPerUnit = I / NP;
 constexpr int kSharedPairs = 2;           // router launch: shared pairs per wave
 constexpr int kSharedBlocks = I / (4 * kSharedPairs);  // 64
-constexpr int kDownRowPairs = 2;          // down: row pairs per wave
-constexpr int kDownRows = 2 * kDownRowPairs;
-constexpr int kDownWavesPerToken = H / kDownRows;      // 512
+
 template <int BITS>
 struct Shape {
   static constexpr int VPC = BITS == 8 ? 16 : 32;   // values per 16-byte chunk
@@ -1214,12 +1212,12 @@ __global__ __launch_bounds__(256) void down_kernel(const DecodeArgs p,
 }
 
 // ------------------------------------------------- few tokens: gate/up, down
-// Every wave of these kernels is resident at once, but a wave keeps only a
-// window of its rows in flight (kWindow pairs / units beyond the one it
-// computes) and issues the next as it consumes one.  With all rows requested at once the memory system
-// served every wave's first row late (measured: the first of 8 pairs landed
-// a median 7.8 us into a 16 us kernel) and the dequantisation ran after the
-// stream instead of under it.
+// Every wave of the gate/up kernel is resident at once, but a wave keeps
+// only a window of its rows in flight (kWindow pairs beyond the one it
+// computes) and issues the next as it consumes one.  With all rows requested
+// at once the memory system served every wave's first row late (measured:
+// the first of 8 pairs landed a median 7.8 us into a 16 us kernel) and the
+// dequantisation ran after the stream instead of under it.
 namespace few {
 constexpr int kWindow = 1;
 }
@@ -1311,154 +1309,117 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// One wave per kDownRows output rows of one token, all its units.  8-bit:
-// lane (r, ch) holds 16-byte chunk ch (16 codes) of rows h0 + 2 rp + r (32
-// lanes a row, RP = 2 row pairs); 4-bit: chunk ch (32 codes) of row h0 + r
-// (16 lanes a row, r < 4, one pass).  With the chunk, the token's bf16
-// activations of it (an L2 hit), unit by unit in a window of kWindow units.
-// Codes become bf16 pairs for v_dot2_f32_bf16 against the packed
-// activations.  COMBINE: weighted sum in slot order, gated shared expert,
-// residual; otherwise per-slot rows y[t, j, h].
-template <int BITS, bool COMBINE>
-__global__ __launch_bounds__(256) void down_few_kernel(const DecodeArgs p) {
+// One workgroup per R output rows of one token, one wave per unit (slot,
+// then the shared expert): wave u issues every load of unit u's
+// rows at once and reduces them (8-bit: 32 lanes a row, 16 codes a lane,
+// two rows per pass; 4-bit: 16 lanes a row, 32 codes a lane, four rows per
+// pass), the codes as bf16 pairs (`v_cvt_f32_ubyte*` and one `v_perm_b32`
+// per two codes: a code has 8 significant bits, so bf16 holds it exactly)
+// for v_dot2_f32_bf16 against the packed bf16 activations; a row's value is
+// fma(bias, sum a, scale * sum q a), rounded to bf16.  COMBINE: the units'
+// rows meet in LDS and lanes 0 .. R - 1 sum them in slot order (weighted),
+// then the residual; otherwise each wave writes its per-slot rows y[t, j, h].
+// R = 16 rows up to 4 tokens, 8 beyond (more, shorter workgroups).
+template <int BITS, bool COMBINE, int R>
+__global__ __launch_bounds__(64 * kMaxFusedUnits) void down_few_kernel(const DecodeArgs p) {
   constexpr int H = few::H;
   constexpr int I = few::I;
   constexpr int NU = kMaxFusedUnits;
-  constexpr int D = few::kWindow;
-  constexpr int LPR = BITS == 8 ? 32 : 16;          // lanes per row
-  constexpr int RPW = 64 / LPR;                      // rows per pass: 2 | 4
-  constexpr int RP = few::kDownRows / RPW;           // passes: 2 | 1
-  constexpr int VPL = BITS == 8 ? 16 : 32;           // values per lane
-  constexpr int WPR = I * BITS / 32;  // words per down row
-  constexpr int GD = I / 64;  // groups per down row
+  constexpr int LPR = BITS == 8 ? 32 : 16;  // lanes per row
+  constexpr int RPW = 64 / LPR;             // rows per pass: 2 | 4
+  constexpr int RP = R / RPW;               // passes
+  constexpr int VPL = BITS == 8 ? 16 : 32;  // values per lane
+  constexpr int WPR = I * BITS / 32;        // words per down row
+  constexpr int GD = I / 64;                // groups per down row
+  constexpr int AV = VPL / 8;               // 16-byte activation pieces per lane
   const int K = p.K;
   const int U1 = K + p.has_shared;
   const int units = COMBINE ? U1 : K;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // (as in gate/up)
+  const int u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's unit
   const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * 4 + wave;
-  const int t = gw / few::kDownWavesPerToken;
-  if (t >= p.T) return;
-  const int h0 = (gw - t * few::kDownWavesPerToken) * few::kDownRows;
+  const int t = blockIdx.x / (H / R);
+  const int h0 = (blockIdx.x - t * (H / R)) * R;
   const int r = lane / LPR;
   const int ch = lane & (LPR - 1);
-  const uint16_t* act =
-      reinterpret_cast<const uint16_t*>(p.act) + (size_t)t * U1 * I + ch * VPL;
-
-  // Experts of the token's slots; an index outside the bank (a caller's)
-  // reads expert 0 and contributes zero.  Loads are issued without branches
-  // around them: a select between a loaded value and a constant made the
-  // compiler convert the loaded value at once, waiting for the whole window.
-  // Units past the call's last (K + shared < 9) re-read the last unit's
-  // rows (cache hits) and are not computed: no branch around any load
-  // (paths that reach a wait with different loads in flight made the
-  // compiler wait for all of them).
-  int ev[NU], ua[NU];
-  bool ush[NU];
-  uint32_t bad = 0;
-#pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    if (u < units || u == 0) {
-      int e = 0;
-      if (u < K) {
-        e = p.idx[t * K + u];
-        const bool ok = (unsigned)e < (unsigned)p.E;
-        bad |= ok ? 0u : 1u << u;
-        e = ok ? e : 0;
-      }
-      ev[u] = e;
-      ush[u] = u >= K;
-      ua[u] = u;
-    } else {
-      ev[u] = ev[u - 1];
-      ush[u] = ush[u - 1];
-      ua[u] = ua[u - 1];
-    }
-  }
-  const QW dn = p.dn, sdn = p.sdn;
-  // the combine weights, loaded ahead of the rows (loaded in the loop, a
-  // wait for one was a wait for the window behind it)
+  __shared__ float s_y[NU][R];
+  // the combine weights of the combining lanes, loaded first
   float score[NU];
+  if (COMBINE && threadIdx.x < R) {
 #pragma unroll
-  for (int u = 0; u < NU; ++u)
-    score[u] = (COMBINE && u < units) ? p.scores[t * p.score_stride + u] : 0.0f;
-  constexpr int AV = VPL / 8;  // 16-byte activation pieces per lane
-  uint4 av[NU][AV];
-  uint4 wv[NU][RP];
-  uint32_t sv[NU][RP], bv[NU][RP];
-  auto issue = [&](int u) {
+    for (int v = 0; v < NU; ++v) score[v] = p.scores[t * p.score_stride + min(v, units - 1)];
+  }
+  if (u < units) {
+    // an index outside the bank (a caller's) reads expert 0 and gives zeros
+    int e = 0;
+    bool bad = false;
+    if (u < K) {
+      e = p.idx[t * K + u];
+      bad = (unsigned)e >= (unsigned)p.E;
+      e = bad ? 0 : e;
+    }
+    const QW q = u < K ? p.dn : p.sdn;
+    const uint16_t* act =
+        reinterpret_cast<const uint16_t*>(p.act) + ((size_t)t * U1 + u) * I + ch * VPL;
+    uint4 av[AV], wv[RP];
+    uint32_t sv[RP], bv[RP];
 #pragma unroll
-    for (int i = 0; i < AV; ++i) av[u][i] = load16(act + ua[u] * I + 8 * i);
-    const QW& q = ush[u] ? sdn : dn;
+    for (int i = 0; i < AV; ++i) av[i] = load16(act + 8 * i);
 #pragma unroll
     for (int rp = 0; rp < RP; ++rp) {
-      const size_t row = (size_t)ev[u] * H + h0 + RPW * rp + r;
-      wv[u][rp] = load16_stream(q.w + row * WPR + ch * 4);
-      sv[u][rp] = q.s[row * GD + (ch * VPL >> 6)];
-      bv[u][rp] = q.b[row * GD + (ch * VPL >> 6)];
+      const size_t row = (size_t)e * H + h0 + RPW * rp + r;
+      wv[rp] = load16_stream(q.w + row * WPR + ch * 4);
+      sv[rp] = q.s[row * GD + (ch * VPL >> 6)];
+      bv[rp] = q.b[row * GD + (ch * VPL >> 6)];
     }
-  };
+    constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
+    uint32_t aw[VPL / 2];
 #pragma unroll
-  for (int u = 0; u < D; ++u) issue(u);
-
-  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
-  float acc[RP] = {};
+    for (int i = 0; i < AV; ++i) {
+      aw[4 * i] = av[i].x;
+      aw[4 * i + 1] = av[i].y;
+      aw[4 * i + 2] = av[i].z;
+      aw[4 * i + 3] = av[i].w;
+    }
+    float asum = 0.0f;
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    if (u + D < NU) issue(u + D);
-    issue_fence();
-    if (u < units) {  // wave-uniform
-      uint32_t aw[VPL / 2];
+    for (int k = 0; k < VPL / 2; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
 #pragma unroll
-      for (int i = 0; i < AV; ++i) {
-        aw[4 * i] = av[u][i].x;
-        aw[4 * i + 1] = av[u][i].y;
-        aw[4 * i + 2] = av[u][i].z;
-        aw[4 * i + 3] = av[u][i].w;
-      }
-      float asum = 0.0f;
+    for (int rp = 0; rp < RP; ++rp) {
+      const uint32_t ww[4] = {wv[rp].x, wv[rp].y, wv[rp].z, wv[rp].w};
+      float dot = 0.0f;
 #pragma unroll
-      for (int k = 0; k < VPL / 2; ++k) asum = dot2_bf16(aw[k], kOnes, asum);
-#pragma unroll
-      for (int rp = 0; rp < RP; ++rp) {
-        const uint32_t ww[4] = {wv[u][rp].x, wv[u][rp].y, wv[u][rp].z, wv[u][rp].w};
-        float dot = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          if constexpr (BITS == 8) {
-            dot = dot2_bf16(codes_bf16x2(ww[k], 0), aw[2 * k], dot);
-            dot = dot2_bf16(codes_bf16x2(ww[k], 1), aw[2 * k + 1], dot);
-          } else {
-            const uint32_t lo = ww[k] & 0x0F0F0F0Fu, hi = (ww[k] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dot = dot2_bf16(nibbles_bf16x2(lo, hi, j), aw[4 * k + j], dot);
-          }
-        }
-        // converted here, not where they are loaded (which waited for them)
-        uint32_t sw = sv[u][rp], bw = bv[u][rp];
-        asm volatile("" : "+v"(sw), "+v"(bw));
-        float y = bf16_to_f32(sw) * dot + bf16_to_f32(bw) * asum;
-        y = round_bf16(segment_sum_fast(y, LPR));
-        y = (bad >> u) & 1u ? 0.0f : y;
-        if constexpr (COMBINE) {
-          acc[rp] += score[u] * y;
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (BITS == 8) {
+          dot = dot2_bf16(codes_bf16x2(ww[k], 0), aw[2 * k], dot);
+          dot = dot2_bf16(codes_bf16x2(ww[k], 1), aw[2 * k + 1], dot);
         } else {
-          if (ch == 0)
-            p.out[((size_t)t * K + u) * H + h0 + RPW * rp + r] = (uint16_t)f32_to_bf16(y);
+          const uint32_t lo = ww[k] & 0x0F0F0F0Fu, hi = (ww[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dot = dot2_bf16(nibbles_bf16x2(lo, hi, j), aw[4 * k + j], dot);
         }
       }
+      float y = fmaf(bf16_to_f32(bv[rp]), asum, bf16_to_f32(sv[rp]) * dot);
+      y = round_bf16(segment_sum_fast(y, LPR));
+      y = bad ? 0.0f : y;
+      if (ch == 0) {
+        if constexpr (COMBINE)
+          s_y[u][RPW * rp + r] = y;
+        else
+          p.out[((size_t)t * K + u) * H + h0 + RPW * rp + r] = (uint16_t)f32_to_bf16(y);
+      }
     }
-    issue_fence();
   }
   if constexpr (COMBINE) {
-    if (ch == 0) {
+    __syncthreads();
+    if (threadIdx.x < R) {
+      const int h = h0 + threadIdx.x;
+      float acc = 0.0f;
 #pragma unroll
-      for (int rp = 0; rp < RP; ++rp) {
-        const int h = h0 + RPW * rp + r;
-        float o = round_bf16(acc[rp]);
-        if (p.residual) o = round_bf16(bf16_to_f32(p.residual[(size_t)t * H + h]) + o);
-        p.out[(size_t)t * H + h] = (uint16_t)f32_to_bf16(o);
-      }
+      for (int v = 0; v < NU; ++v)
+        if (v < units) acc = fmaf(score[v], s_y[v][threadIdx.x], acc);
+      float o = round_bf16(acc);
+      if (p.residual) o = round_bf16(bf16_to_f32(p.residual[(size_t)t * H + h]) + o);
+      p.out[(size_t)t * H + h] = (uint16_t)f32_to_bf16(o);
     }
   }
 }
@@ -1657,17 +1618,28 @@ hipError_t launch_gate_up(const DecodeArgs& a, int bits, hipStream_t s) {
 
 hipError_t launch_down(const DecodeArgs& a, int bits, bool combine, hipStream_t s) {
   if (a.few_bits != 0) {
-    const dim3 grid((unsigned)(a.T * few::kDownWavesPerToken / 4));
+    // rows per workgroup: 16 up to 4 tokens, 8 beyond
+    const dim3 block(64 * kMaxFusedUnits);
+    auto go = [&](auto bits_c, auto combine_c, auto r_c) {
+      constexpr int B = decltype(bits_c)::value;
+      constexpr bool C = decltype(combine_c)::value;
+      constexpr int R = decltype(r_c)::value;
+      hipLaunchKernelGGL((down_few_kernel<B, C, R>), dim3((unsigned)(a.T * (few::H / R))), block,
+                         0, s, a);
+    };
+    using B8 = std::integral_constant<int, 8>;
+    using B4 = std::integral_constant<int, 4>;
+    using CT = std::true_type;
+    using CF = std::false_type;
+    using R16 = std::integral_constant<int, 16>;
+    using R8 = std::integral_constant<int, 8>;
+    const bool wide = a.T <= 4;
     if (a.few_bits == 8) {
-      if (combine)
-        hipLaunchKernelGGL((down_few_kernel<8, true>), grid, dim3(256), 0, s, a);
-      else
-        hipLaunchKernelGGL((down_few_kernel<8, false>), grid, dim3(256), 0, s, a);
+      if (combine) wide ? go(B8{}, CT{}, R16{}) : go(B8{}, CT{}, R8{});
+      else wide ? go(B8{}, CF{}, R16{}) : go(B8{}, CF{}, R8{});
     } else {
-      if (combine)
-        hipLaunchKernelGGL((down_few_kernel<4, true>), grid, dim3(256), 0, s, a);
-      else
-        hipLaunchKernelGGL((down_few_kernel<4, false>), grid, dim3(256), 0, s, a);
+      if (combine) wide ? go(B4{}, CT{}, R16{}) : go(B4{}, CT{}, R8{});
+      else wide ? go(B4{}, CF{}, R16{}) : go(B4{}, CF{}, R8{});
     }
     RMOE_CHECK_LAUNCH();
     return hipSuccess;
