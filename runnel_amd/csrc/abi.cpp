@@ -336,6 +336,7 @@ rmoe::DecodeArgs decode_args(const rmoe_layer* L, const uint16_t* x, int T,
   a.score_stride = a.K + 1;
   a.act = reinterpret_cast<float*>(base + l.act);
   a.ctr = reinterpret_cast<uint32_t*>(base + l.ctr);
+  a.fs = reinterpret_cast<rmoe::FusedScratch*>(base + l.fused);
   return a;
 }
 

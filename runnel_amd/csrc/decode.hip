@@ -13,6 +13,7 @@
 //                   are summed in registers, bf16 written once.
 //   qmv_kernel      plain gather-QMV (mx.gather_qmm at M rows).
 #include "common.h"
+#include "handover.h"
 #include "kernels.h"
 
 namespace rmoe {
@@ -34,8 +35,8 @@ constexpr int G = H / 64;                 // groups per gate/up row (32)
 // layers from HBM, us per layer call: 8 pairs 42.0, 4 pairs 34.7, 2 pairs 30.5)
 constexpr int NP = 2;
 constexpr int kWavesPerUnit = I / NP;
-constexpr int kSharedPairs = 2;           // router launch: shared pairs per wave
-constexpr int kSharedBlocks = I / (4 * kSharedPairs);  // 64
+constexpr int kSharedPairs = 1;           // router launch: shared pairs per wave
+constexpr int kSharedBlocks = I / (4 * kSharedPairs);  // 128
 
 template <int BITS>
 struct Shape {
@@ -383,7 +384,14 @@ __device__ __forceinline__ void q8_gate_partials(const QW& bank, size_t row, con
 
 // One wave per router row and group of TB tokens (grid.y): the row is
 // streamed once for the group.  The last workgroup of a group ranks its
-// tokens, one wave per token.
+// tokens, one wave per token.  With the few-token kernels (SB != 0) the
+// logits go over as tagged words instead (bf16 | tag of the call, read from
+// the epoch word, which the gate/up launch after this one advances): each
+// row's wave stores its words without waiting for them to land, and
+// workgroup 0 of the group polls its tokens' words (bounded, like every
+// wait of the single-launch decode; a failed wait sets the status word) and
+// ranks them as soon as they are in, one wave per token: no acknowledged
+// stores, no counter.
 template <int P, int TB, int SB>
 __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   static_assert(TB >= 1 && TB <= 4, "one ranking wave per token");
@@ -408,6 +416,10 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   const int R = p.E + has_sg;
   const int row = blockIdx.x * 4 + wave;
   const size_t ls = (size_t)(p.E + 1);
+  uint32_t* const words = reinterpret_cast<uint32_t*>(p.logits);
+  uint32_t base = 0;
+  if constexpr (SB != 0) base = load_coherent_u32(&p.fs->epoch);
+  const uint32_t tag = phase_tag(base + 1);
   if (row < R) {
     float acc[TB];
     const uint16_t* xt = p.x + (size_t)t0 * p.H;
@@ -421,9 +433,66 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
     for (int k = 0; k < TB; ++k) {
       if (k < nt) {
         const float v = wave_sum(acc[k]);
-        if (lane == 0) store_coherent(p.logits + (t0 + k) * ls + row, v);
+        if (lane == 0) {
+          if constexpr (SB != 0)
+            store_coherent_u32(words + (t0 + k) * ls + row, tagged(f32_to_bf16(v), tag));
+          else
+            store_coherent(p.logits + (t0 + k) * ls + row, v);
+        }
       }
     }
+  }
+
+  if constexpr (SB != 0) {
+    // Workgroup 0 of the group: wave w ranks token t0 + w.
+    if (blockIdx.x != 0 || wave >= nt) return;
+    const int t = t0 + wave;
+    const uint32_t* lw = words + t * ls;
+    WaitState ws{p.fs, base + 1, false};
+    // a call whose key the host has written into the abort word beforehand
+    // waits for nothing (status 1)
+    if (load_coherent_u32(&p.fs->abort) == ws.key) {
+      ws.gave_up = true;
+      if (lane == 0) publish_failure(p.fs, ws.key, 1u);
+    }
+    uint32_t w[P], wsg = 0;
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      w[i] = 0;
+      if (lane + 64 * i < p.E) pend |= 1u << i;
+    }
+    if (lane == 0 && has_sg) pend |= 1u << P;
+    if (ws.gave_up) pend = 0;
+    for (int spin = 0;; ++spin) {
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if ((pend >> i) & 1u) w[i] = load_coherent_u32(lw + lane + 64 * i);
+      if ((pend >> P) & 1u) wsg = load_coherent_u32(lw + p.E);
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (((pend >> i) & 1u) && tag_ok(w[i], tag)) pend &= ~(1u << i);
+      if (((pend >> P) & 1u) && tag_ok(wsg, tag)) pend &= ~(1u << P);
+      if (!__any(pend != 0u)) break;
+      if (give_up(ws, spin)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    float lv[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      lv[i] = lane + 64 * i < p.E ? __uint_as_float(w[i] & 0xFFFF0000u) : 0.0f;
+    // Every word seen is cleared (tag 0 is never current), so a later call
+    // can only find 0 or its own words there, whatever its tag; a word
+    // still pending after a failed wait stays (the epoch moves on).
+    if (!ws.gave_up) {
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (lane + 64 * i < p.E) store_coherent_u32(words + t * ls + lane + 64 * i, 0u);
+      if (lane == 0 && has_sg) store_coherent_u32(words + t * ls + p.E, 0u);
+    }
+    // (lane 0 holds the shared gate's word; only lane 0 uses it)
+    finish_route<P>(p, t, lv, __uint_as_float(wsg & 0xFFFF0000u));
+    return;
   }
 
   // Last workgroup of this token group ranks the logits.
@@ -1238,6 +1307,9 @@ __global__ __launch_bounds__(256) void gate_up_few_kernel(const DecodeArgs p) {
   // wait on it a wait for the whole window)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  // the router launch before this one has finished with the call's tag
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    store_coherent_u32(&p.fs->epoch, load_coherent_u32(&p.fs->epoch) + 1);
   const int gw = blockIdx.x * 4 + wave;
   const int m = gw / few::kWavesPerUnit;
   if (m >= TK) return;

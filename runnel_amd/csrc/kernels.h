@@ -22,6 +22,8 @@ struct QW {
   const uint16_t* b;
 };
 
+struct FusedScratch;
+
 // One decode-shaped call: T tokens, K routed slots, an optional shared
 // expert (unit K of every token).
 struct DecodeArgs {
@@ -47,6 +49,7 @@ struct DecodeArgs {
   const uint16_t* residual;
   int32_t* idx_out;
   float* scores_out;
+  FusedScratch* fs;  // epoch and status words (the few-token router's tagged hand-over)
 };
 
 struct QmvArgs {

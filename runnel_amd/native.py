@@ -301,13 +301,15 @@ def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None
     """Whole SparseMoeBlock on x bf16 [T, H] -> bf16 [T, H].
 
     ``check``: True reads (and clears) the workspace's status word after the
-    call and raises RmoeError (RMOE_ETIMEOUT / RMOE_EPLACEMENT) if the
-    single-launch decode failed; this synchronises the stream.  None (the
-    default) checks eager one-token calls without waiting for the device:
-    behind the first call on a workspace and every 32nd after it, the word
-    is copied to pinned host memory, and a later eager call on the
-    workspace examines the copy once it has landed and raises then.  False skips the check; graph
-    users call ``check_status`` on the workspace after a replay."""
+    call and raises RmoeError (RMOE_ETIMEOUT / RMOE_EPLACEMENT) if a bounded
+    wait of the call gave up (the single-launch decode, the few-token
+    router); this synchronises the stream.  None (the default) checks eager
+    calls below the expert-sorted threshold (T * top_k < 64) without
+    waiting for the device: behind the first call on a workspace and every
+    32nd after it, the word is copied to pinned host memory, and a later
+    eager call on the workspace examines the copy once it has landed and
+    raises then.  False skips the check; graph users call ``check_status``
+    on the workspace after a replay."""
     lib = _lib.load()
     H = layer.hidden
     _check_x(x, H)
@@ -328,7 +330,7 @@ def moe_block(layer: LayerHandle, x: torch.Tensor, residual: torch.Tensor | None
         scores = torch.empty((T, layer.top_k), dtype=torch.float32, device=x.device)
     need = layer.workspace_bytes(T)
     ws = workspace if workspace is not None else WORKSPACE.get(x.device, need, "block")
-    deferred = check is None and T == 1 and not _capturing(x.device)
+    deferred = check is None and T * layer.top_k < _SORTED_ROWS and not _capturing(x.device)
     if deferred:
         _STATUS.poll(ws)
     _lib.check(lib.rmoe_moe_block(ctypes.byref(layer.struct), x.data_ptr(), T,
@@ -400,6 +402,9 @@ def moe_chain(chain: Chain, x: torch.Tensor, out: torch.Tensor | None = None,
 # The launch mode last set through set_cooperative_launch (the library's
 # default is a plain launch).
 _COOPERATIVE = [False]
+# (token, slot) rows from which a block call takes the expert-sorted path,
+# whose kernels do not wait on each other (src/runnel/mlx.py:59)
+_SORTED_ROWS = 64
 
 
 def _capturing(device) -> bool:

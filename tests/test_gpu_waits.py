@@ -9,7 +9,8 @@ them, run on the GPU through the C ABI (native wrappers):
   the next call on the workspace is correct;
 * the 16-bit phase tags wrapping around, and a call with more routed slots
   after calls with fewer (every hand-over word is rewritten in every layer,
-  so no word left by an older call can carry the current tag).
+  so no word left by an older call can carry the current tag);
+* the few-token router's tagged logits across the wrap, and cancelled.
 
 Outputs are compared bit for bit with the same calls made in the ordinary
 way (cooperative launches, fresh epochs), which the oracle tests pin."""
@@ -185,3 +186,47 @@ def test_deferred_status_check_raises_within_the_period(torch_cuda, layer8):
     native.moe_block(h, x, workspace=ws)
     torch.cuda.synchronize()
     assert native.workspace_status(ws) == 0
+
+
+def test_few_token_router_hand_over(torch_cuda):
+    """The few-token router hands its logits over as tagged words: 4-token
+    calls across the 65535-phase wrap of the tags equal the first call bit
+    for bit; a call cancelled through the abort word returns promptly with
+    the status word at 1, and the next call is correct again."""
+    torch = torch_cuda
+    from runnel_amd import _lib, native, synthetic
+    lw = synthetic.make_layer(6200, bits=8)
+    h = lw.handle()
+    x = synthetic.make_x(6201, 4, 2048)
+    ws = torch.zeros(h.workspace_bytes(4), dtype=torch.uint8, device="cuda")
+    ref = native.moe_block(h, x, workspace=ws, check=False).clone()
+    torch.cuda.synchronize()
+    assert native.workspace_status(ws) == 0
+    w = _words(ws, torch)
+    w[0].fill_(65532)
+    for i in range(5):
+        got = native.moe_block(h, x, workspace=ws, check=False)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"call {i} across the wrap"
+    assert native.workspace_status(ws) == 0
+    t0 = time.perf_counter()
+    native.moe_block(h, x, workspace=ws, check=False)
+    torch.cuda.synchronize()
+    t_ok = time.perf_counter() - t0
+    epoch = int(w[0].item())
+    w[2].fill_(epoch + 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    native.moe_block(h, x, workspace=ws, check=False)
+    torch.cuda.synchronize()
+    t_cancel = time.perf_counter() - t0
+    print(f"cancelled 4-token call {t_cancel * 1e6:.0f} us, ordinary {t_ok * 1e6:.0f} us",
+          flush=True)
+    assert t_cancel < max(20 * t_ok, 0.05)
+    with pytest.raises(_lib.RmoeError) as e:
+        native.check_status(ws)
+    assert e.value.status == _lib.RMOE_ETIMEOUT
+    again = native.moe_block(h, x, workspace=ws, check=False)
+    torch.cuda.synchronize()
+    assert native.workspace_status(ws) == 0
+    assert torch.equal(again, ref)
