@@ -416,7 +416,10 @@ __global__ __launch_bounds__(256) void router_kernel(const DecodeArgs p) {
   const int R = p.E + has_sg;
   const int row = blockIdx.x * 4 + wave;
   const size_t ls = (size_t)(p.E + 1);
-  uint32_t* const words = reinterpret_cast<uint32_t*>(p.logits);
+  // (the few-token path's words: their own area of the single-launch
+  // scratch, never written by the other routers, whose fp32 logits could
+  // carry any low half)
+  uint32_t* const words = SB != 0 ? &p.fs->few[0][0] : reinterpret_cast<uint32_t*>(p.logits);
   uint32_t base = 0;
   if constexpr (SB != 0) base = load_coherent_u32(&p.fs->epoch);
   const uint32_t tag = phase_tag(base + 1);

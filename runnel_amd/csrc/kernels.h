@@ -100,6 +100,10 @@ struct FusedScratch {
   uint32_t sact[2][kFusedI];                  // shared activations, by layer parity
   uint32_t ys[2][kMaxFusedUnits][kFusedH];    // unit outputs, by layer parity
   uint32_t xl[8][2][kFusedH];                 // combined layer input of XCD x, by parity
+  // the few-token router's logits, as tagged words (token t, expert e; the
+  // shared gate's at e = E): only that router writes here, and its ranking
+  // workgroup clears every word it has read
+  uint32_t few[kFewMaxTokens][kFusedMaxExperts + 1];
 };
 
 struct FusedArgs {

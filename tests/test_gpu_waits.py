@@ -230,3 +230,37 @@ def test_few_token_router_hand_over(torch_cuda):
     torch.cuda.synchronize()
     assert native.workspace_status(ws) == 0
     assert torch.equal(again, ref)
+
+
+def test_few_token_words_apart_from_other_routers(torch_cuda):
+    """The few-token router's tagged words have an area of their own: a
+    general-path call on the same workspace leaves its fp32 logits and int32
+    expert ids (small integers, which equal a tag at the right epoch) where
+    it keeps them, and a few-token call whose tag equals each such id still
+    equals the same call on a fresh workspace."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    from helpers import dev_bf16, layer_to_dev
+    from oracle import moe_ref as M
+    few = synthetic.make_layer(6300, bits=8)
+    hf = few.handle()
+    small = layer_to_dev(M.make_layer(6301, hidden=512, inter=128, experts=32, top_k=4, bits=8))
+    xf = synthetic.make_x(6302, 4, 2048)
+    xs = dev_bf16(M.make_x(6303, 4, 512))
+    need = max(hf.workspace_bytes(4), small.workspace_bytes(4))
+    ref = native.moe_block(hf, xf, workspace=torch.zeros(need, dtype=torch.uint8, device="cuda"),
+                           check=False).clone()
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    w = _words(ws, torch)
+    _, idx, _ = native.moe_block(small, xs, workspace=ws, return_routing=True, check=False)
+    torch.cuda.synchronize()
+    ids = sorted({int(v) for v in idx.flatten().tolist() if int(v) >= 2})
+    assert ids
+    for e in ids[:6]:
+        native.moe_block(small, xs, workspace=ws, check=False)
+        torch.cuda.synchronize()
+        w[0].fill_(e - 2)  # the next few-token call's tag is e
+        got = native.moe_block(hf, xf, workspace=ws, check=False)
+        torch.cuda.synchronize()
+        assert native.workspace_status(ws) == 0
+        assert torch.equal(got, ref), f"tag {e}"
