@@ -265,15 +265,17 @@ int rmoe_moe_chain(const rmoe_layer* layer0, const void* device_table,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Byte offset inside a workspace of a uint32 status word: nonzero when a
- * single-launch decode failed (the call still completes; its outputs are then
- * not valid): 1 when a workgroup gave up a cross-workgroup wait (every wait
- * is bounded, and the other workgroups of the call stop waiting as soon as
- * one gives up), 2 when a workgroup read an XCC id outside 0-7.  The word is
- * sticky: later calls leave it set until the caller
- * clears it.  The uint32 before it holds the workspace's phase epoch and the
- * one after it the abort word: a caller cancels the next single-launch call
- * on the workspace before it runs by writing epoch + 1 there (the call then
- * waits for nothing and sets the status word to 1). */
+ * single-launch decode or a few-token call (2-8 tokens at the single-launch
+ * shapes, whose router hands its logits over between workgroups) failed
+ * (the call still completes; its outputs are then not valid): 1 when a
+ * workgroup gave up a cross-workgroup wait (every wait is bounded, and the
+ * other workgroups of the call stop waiting as soon as one gives up), 2 when
+ * a workgroup read an XCC id outside 0-7.  The word is sticky: later calls
+ * leave it set until the caller clears it.  The uint32 before it holds the
+ * workspace's phase epoch and the one after it the abort word: a caller
+ * cancels the next such call on the workspace before it runs by writing
+ * epoch + 1 there (the call then waits for nothing and sets the status word
+ * to 1). */
 size_t rmoe_workspace_status_offset(void);
 
 /* Launch mode of the single-launch decode kernel (rmoe_moe_block with one
