@@ -66,7 +66,9 @@ def _same(torch, a, b):
 @pytest.mark.parametrize("bits", [8, 4])
 def test_noalloc_full_layer_prefill_then_decode(torch_cuda, bits):
     """A full-size layer: 40 tokens (the expert-sorted matrix-core path),
-    then one token (the single-launch decode kernel) with a residual."""
+    then one token (the single-launch decode kernel) with a residual, then
+    4 tokens (the few-token kernels, whose router hands its logits over in
+    the static scratch)."""
     torch = torch_cuda
     from runnel_amd import synthetic
     print(f"noalloc full layer bits={bits}", flush=True)
@@ -77,6 +79,9 @@ def test_noalloc_full_layer_prefill_then_decode(torch_cuda, bits):
     x1 = synthetic.make_x(8802, 1, 2048)
     r1 = synthetic.make_x(8803, 1, 2048)
     _same(torch, _noalloc(torch, h, x1, r1), _with_workspace(torch, h, x1, r1))
+    x4 = synthetic.make_x(8804, 4, 2048)
+    for _ in range(2):
+        _same(torch, _noalloc(torch, h, x4), _with_workspace(torch, h, x4))
 
 
 def test_noalloc_small_layer_few_tokens(torch_cuda):
