@@ -883,15 +883,22 @@ __device__ __forceinline__ float check_dot(const uint4 (&xv)[XC], const CheckRow
 // per token): the token row stays unpacked as floats, which costs
 // occupancy (5 waves per SIMD) but 32 fewer instructions per row
 // (8192 tokens 32.4 -> 27.8 us, 512 tokens 13.3 -> 11.2).
-template <int RQ, int XC>
+// WPT = 4 (fewer tokens than the device has SIMDs): one workgroup per
+// token; wave 0 finds the threshold and the list, the four waves re-check
+// every fourth listed row each (the dots go to LDS), wave 0 ranks.
+template <int RQ, int XC, int WPT>
 __global__ __launch_bounds__(256) 
 void router_select_kernel(const DecodeArgs p, const float* wnorm) {
+  static_assert(WPT == 1 || WPT == 4, "a wave per token, or a workgroup");
   constexpr int P = 4;
-  __shared__ int s_list[4][P * 64 + 1];
+  __shared__ int s_list[WPT == 1 ? 4 : 1][P * 64 + 1];
+  __shared__ float s_c[WPT == 1 ? 1 : P * 64 + 1];
+  __shared__ int s_n;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
+  const int t = WPT == 1 ? blockIdx.x * 4 + wave : blockIdx.x;
   if (t >= p.T) return;
+  const bool lead = WPT == 1 || wave == 0;  // finds the list and ranks
   const int H = p.H;
   const float* lg = p.logits + (size_t)t * (p.E + 1);
   const uint16_t* xt = p.x + (size_t)t * H;
@@ -913,7 +920,11 @@ void router_select_kernel(const DecodeArgs p, const float* wnorm) {
       xv[c] = load16(xt + (lane + 64 * (c < (H >> 9) ? c : 0)) * 8);
     }
   }
-  if (p.has_sg) check_load<RQ, XC>(ra, row_ptr(p.E), row_bank(p.E), 0, H, lane);
+  if (p.has_sg && lead) check_load<RQ, XC>(ra, row_ptr(p.E), row_bank(p.E), 0, H, lane);
+  int n = 0;
+  float out[P];
+  int* const list = s_list[WPT == 1 ? wave : 0];
+  if (lead) {
   // logits and row bounds: unconditional loads (lanes past E read expert
   // E - 1), so that all of them are in flight together
   float lraw[P], wraw[P];
@@ -962,12 +973,10 @@ void router_select_kernel(const DecodeArgs p, const float* wnorm) {
   const float ulp = __uint_as_float((uint32_t)max(ex - 7, 1) << 23);
   const float margin = (2.0f * delta + 1.25f * ulp) * (1.0f + 0x1p-20f);
   const float lo = tk - margin;
-  float out[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) out[i] = lane + 64 * i < p.E ? round_bf16(lv[i]) : 0.0f;
   // the list: the shared gate, then the experts within the margin in index order
-  int* list = s_list[wave];
-  int n = p.has_sg ? 1 : 0;
+  n = p.has_sg ? 1 : 0;
   if (p.has_sg && lane == 0) list[0] = p.E;
 #pragma unroll
   for (int i = 0; i < P; ++i) {
@@ -978,7 +987,21 @@ void router_select_kernel(const DecodeArgs p, const float* wnorm) {
         lane + 64 * i;
     n += __popcll(m);
   }
-  __builtin_amdgcn_wave_barrier();
+  if (WPT > 1 && lane == 0) s_n = n;
+  } else {
+    // the other waves only re-check: zero the pieces past the row's end
+#pragma unroll
+    for (int c = 0; c < XC; ++c) {
+      const bool live = RQ ? lane + 64 * (c >> 1) < (H >> 4) : c < (H >> 9);
+      if (!live) xv[c] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  if constexpr (WPT > 1) {
+    __syncthreads();
+    n = s_n;
+  } else {
+    __builtin_amdgcn_wave_barrier();
+  }
   float sg_logit = 0.0f;
   auto record = [&](int code, float c) {
     if (code >= p.E) {
@@ -989,20 +1012,35 @@ void router_select_kernel(const DecodeArgs p, const float* wnorm) {
         if ((code >> 6) == i && lane == (code & 63)) out[i] = round_bf16(c);
     }
   };
+  // this wave's rows: list[j] for j = first, first + WPT, ... (n = 0 only
+  // for NaN logits); the lead wave's ra holds the shared gate's row,
+  // list[0], already
+  const int first = WPT == 1 ? 0 : wave;
+  auto emit = [&](int j, int code, float c) {
+    if constexpr (WPT == 1)
+      record(code, c);
+    else if (lane == 0)
+      s_c[j] = c;
+  };
   int ca = p.E;
-  if (!p.has_sg && n > 0) {  // n = 0 only for NaN logits
-    ca = __builtin_amdgcn_readfirstlane(list[0]);
+  if (!(p.has_sg && lead) && first < n) {
+    ca = __builtin_amdgcn_readfirstlane(list[first]);
     check_load<RQ, XC>(ra, row_ptr(ca), row_bank(ca), row_index(ca), H, lane);
   }
-  for (int j = 0; j < n; j += 2) {
-    const int cb = __builtin_amdgcn_readfirstlane(list[min(j + 1, n - 1)]);
+  for (int j = first; j < n; j += 2 * WPT) {
+    const int cb = __builtin_amdgcn_readfirstlane(list[min(j + WPT, n - 1)]);
     check_load<RQ, XC>(rb, row_ptr(cb), row_bank(cb), row_index(cb), H, lane);
-    record(ca, check_dot<RQ, XC>(xv, ra, H, lane));
-    if (j + 1 >= n) break;
-    const int cn = __builtin_amdgcn_readfirstlane(list[min(j + 2, n - 1)]);
+    emit(j, ca, check_dot<RQ, XC>(xv, ra, H, lane));
+    if (j + WPT >= n) break;
+    const int cn = __builtin_amdgcn_readfirstlane(list[min(j + 2 * WPT, n - 1)]);
     check_load<RQ, XC>(ra, row_ptr(cn), row_bank(cn), row_index(cn), H, lane);
-    record(cb, check_dot<RQ, XC>(xv, rb, H, lane));
+    emit(j + WPT, cb, check_dot<RQ, XC>(xv, rb, H, lane));
     ca = cn;
+  }
+  if constexpr (WPT > 1) {
+    __syncthreads();
+    if (!lead) return;
+    for (int j = 0; j < n; ++j) record(list[j], s_c[j]);
   }
   finish_route<P>(p, t, out, sg_logit);
 }
@@ -1578,6 +1616,19 @@ bool router_mfma_eligible(int E, int H) {
 // 64 x 64 tiles (two workgroups of four waves per CU) from 4096 tokens on,
 // 32 x 32 below, where 64-token tiles leave most CUs idle: at 512 tokens
 // 11.7 against 17.3 us, at 8192 tokens 21.2 against 32.2 (event-timed).
+// The selection: a workgroup per token while the tokens number at most the
+// device's 1024 SIMDs (the re-checks of a token then run on four waves),
+// else a wave per token.
+template <int RQ, int XC>
+static void select_launch(const DecodeArgs& a, const void* wnorm, hipStream_t s) {
+  if (a.T <= 1024)
+    hipLaunchKernelGGL((router_select_kernel<RQ, XC, 4>), dim3(a.T), dim3(256), 0, s, a,
+                       (const float*)wnorm);
+  else
+    hipLaunchKernelGGL((router_select_kernel<RQ, XC, 1>), dim3((a.T + 3) / 4), dim3(256), 0, s,
+                       a, (const float*)wnorm);
+}
+
 template <bool ACC, bool WNORM>
 static void launch_logits(const DecodeArgs& a, float* wnorm, hipStream_t s) {
   if (a.T >= 4096)
@@ -1600,20 +1651,16 @@ hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split
     launch_logits<false, false>(hi, nullptr, s);
     launch_logits<true, false>(lo, nullptr, s);
     if (a.H <= 2048)
-      hipLaunchKernelGGL((router_select_kernel<1, 4>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                         (const float*)wnorm);
+      select_launch<1, 4>(a, wnorm, s);
     else
-      hipLaunchKernelGGL((router_select_kernel<1, 8>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                         (const float*)wnorm);
+      select_launch<1, 8>(a, wnorm, s);
   } else {
     // the row norms come from the first token tile's workgroups
     launch_logits<false, true>(a, wnorm, s);
     if (a.H <= 2048)
-      hipLaunchKernelGGL((router_select_kernel<0, 4>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                         (const float*)wnorm);
+      select_launch<0, 4>(a, wnorm, s);
     else
-      hipLaunchKernelGGL((router_select_kernel<0, 8>), dim3((a.T + 3) / 4), dim3(256), 0, s, a,
-                         (const float*)wnorm);
+      select_launch<0, 8>(a, wnorm, s);
   }
   RMOE_CHECK_LAUNCH();
   return hipSuccess;
