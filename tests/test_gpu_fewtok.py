@@ -92,3 +92,37 @@ def test_few_token_calls_repeat_bit_exact(torch_cuda, bits):
     b = native.moe_block(h, x4, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_few_token_graph_replays_equal_eager_calls(torch_cuda, bits):
+    """Few-token calls captured in a HIP graph: every replay (the router's
+    tags come from the workspace's epoch, which each call advances on the
+    device) equals the eager calls bit for bit, with eager calls and
+    synchronisations between the replays."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lw = synthetic.make_layer(7100 + bits, bits=bits)
+    h = lw.handle()
+    xa = synthetic.make_x(7101, 4, 2048)
+    xb = synthetic.make_x(7102, 3, 2048)
+    ws = torch.zeros(h.workspace_bytes(4), dtype=torch.uint8, device="cuda")
+    ref_a = native.moe_block(h, xa, workspace=ws, check=False).clone()
+    ref_b = native.moe_block(h, xb, workspace=ws, check=False).clone()
+    oa, ob = torch.empty_like(xa), torch.empty_like(xb)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        native.moe_block(h, xa, out=oa, workspace=ws, check=False)
+        native.moe_block(h, xb, out=ob, workspace=ws, check=False)
+    for r in range(3):
+        oa.zero_()
+        ob.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(oa, ref_a), f"replay {r}"
+        assert torch.equal(ob, ref_b), f"replay {r}"
+        eager = native.moe_block(h, xa, workspace=ws, check=False)
+        torch.cuda.synchronize()
+        assert torch.equal(eager, ref_a)
+    assert native.workspace_status(ws) == 0
