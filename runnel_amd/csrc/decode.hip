@@ -925,69 +925,69 @@ void router_select_kernel(const DecodeArgs p, const float* wnorm) {
   float out[P];
   int* const list = s_list[WPT == 1 ? wave : 0];
   if (lead) {
-  // logits and row bounds: unconditional loads (lanes past E read expert
-  // E - 1), so that all of them are in flight together
-  float lraw[P], wraw[P];
+    // logits and row bounds: unconditional loads (lanes past E read expert
+    // E - 1), so that all of them are in flight together
+    float lraw[P], wraw[P];
 #pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const int e = min(lane + 64 * i, p.E - 1);
-    lraw[i] = lg[e];
-    wraw[i] = wnorm[e];
-  }
-  issue_fence();  // keeps these loads from being sunk into per-lane branches
-  float lv[P], wn = 0.0f, amax = 0.0f;
-  uint32_t key[P];
-#pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const bool on = lane + 64 * i < p.E;
-    lv[i] = on ? lraw[i] : 0.0f;
-    key[i] = on ? f32_order_key(lraw[i]) : 0u;
-    wn = fmaxf(wn, on ? wraw[i] : 0.0f);
-    amax = fmaxf(amax, fabsf(lv[i]));
-  }
-  // pieces past the row's end were loaded as the first piece: zero them
-#pragma unroll
-  for (int c = 0; c < XC; ++c) {
-    const bool live = RQ ? lane + 64 * (c >> 1) < (H >> 4) : c < (H >> 9);
-    if (!live) xv[c] = make_uint4(0, 0, 0, 0);
-    const uint32_t vv[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      nx2 = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), nx2);
-      nx2 = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), nx2);
+    for (int i = 0; i < P; ++i) {
+      const int e = min(lane + 64 * i, p.E - 1);
+      lraw[i] = lg[e];
+      wraw[i] = wnorm[e];
     }
-  }
-  const float nx = sqrtf(wave_sum(nx2)) * (1.0f + 1.0f / 1024.0f);
-  wn = __uint_as_float(wave_max_u32(__float_as_uint(wn)));      // non-negative
-  amax = __uint_as_float(wave_max_u32(__float_as_uint(amax)));
-  // k-th largest L (with multiplicity)
-  const uint32_t thr = wave_kth_largest<P>(key, p.K);
-  const float tk = f32_from_order_key(thr);
-  const float gam =
-      RQ ? (float)(2 * H - 1) * 0x1p-23f * (1.0f + 0x1p-7f) + 0x1p-17f +
-               (float)(15 + 2 * ((H + 1023) / 1024) + 8) * 0x1p-24f
-         : (float)(H - 1) * 0x1p-23f + (float)(H / 64 + 8) * 0x1p-24f;
-  const float delta = gam * nx * wn + 0x1p-100f * (1.0f + nx + wn);
-  const float mag = amax + 2.0f * delta + 1.0f;
-  const int ex = (int)((__float_as_uint(mag) >> 23) & 0xFFu);
-  const float ulp = __uint_as_float((uint32_t)max(ex - 7, 1) << 23);
-  const float margin = (2.0f * delta + 1.25f * ulp) * (1.0f + 0x1p-20f);
-  const float lo = tk - margin;
+    issue_fence();  // keeps these loads from being sunk into per-lane branches
+    float lv[P], wn = 0.0f, amax = 0.0f;
+    uint32_t key[P];
 #pragma unroll
-  for (int i = 0; i < P; ++i) out[i] = lane + 64 * i < p.E ? round_bf16(lv[i]) : 0.0f;
-  // the list: the shared gate, then the experts within the margin in index order
-  n = p.has_sg ? 1 : 0;
-  if (p.has_sg && lane == 0) list[0] = p.E;
+    for (int i = 0; i < P; ++i) {
+      const bool on = lane + 64 * i < p.E;
+      lv[i] = on ? lraw[i] : 0.0f;
+      key[i] = on ? f32_order_key(lraw[i]) : 0u;
+      wn = fmaxf(wn, on ? wraw[i] : 0.0f);
+      amax = fmaxf(amax, fabsf(lv[i]));
+    }
+    // pieces past the row's end were loaded as the first piece: zero them
 #pragma unroll
-  for (int i = 0; i < P; ++i) {
-    const bool in = lane + 64 * i < p.E && lv[i] >= lo;
-    const uint64_t m = __ballot(in);
-    if (in) list[n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
-        lane + 64 * i;
-    n += __popcll(m);
-  }
-  if (WPT > 1 && lane == 0) s_n = n;
+    for (int c = 0; c < XC; ++c) {
+      const bool live = RQ ? lane + 64 * (c >> 1) < (H >> 4) : c < (H >> 9);
+      if (!live) xv[c] = make_uint4(0, 0, 0, 0);
+      const uint32_t vv[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nx2 = fmaf(bf16_lo(vv[i]), bf16_lo(vv[i]), nx2);
+        nx2 = fmaf(bf16_hi(vv[i]), bf16_hi(vv[i]), nx2);
+      }
+    }
+    const float nx = sqrtf(wave_sum(nx2)) * (1.0f + 1.0f / 1024.0f);
+    wn = __uint_as_float(wave_max_u32(__float_as_uint(wn)));      // non-negative
+    amax = __uint_as_float(wave_max_u32(__float_as_uint(amax)));
+    // k-th largest L (with multiplicity)
+    const uint32_t thr = wave_kth_largest<P>(key, p.K);
+    const float tk = f32_from_order_key(thr);
+    const float gam =
+        RQ ? (float)(2 * H - 1) * 0x1p-23f * (1.0f + 0x1p-7f) + 0x1p-17f +
+                 (float)(15 + 2 * ((H + 1023) / 1024) + 8) * 0x1p-24f
+           : (float)(H - 1) * 0x1p-23f + (float)(H / 64 + 8) * 0x1p-24f;
+    const float delta = gam * nx * wn + 0x1p-100f * (1.0f + nx + wn);
+    const float mag = amax + 2.0f * delta + 1.0f;
+    const int ex = (int)((__float_as_uint(mag) >> 23) & 0xFFu);
+    const float ulp = __uint_as_float((uint32_t)max(ex - 7, 1) << 23);
+    const float margin = (2.0f * delta + 1.25f * ulp) * (1.0f + 0x1p-20f);
+    const float lo = tk - margin;
+#pragma unroll
+    for (int i = 0; i < P; ++i) out[i] = lane + 64 * i < p.E ? round_bf16(lv[i]) : 0.0f;
+    // the list: the shared gate, then the experts within the margin in index order
+    n = p.has_sg ? 1 : 0;
+    if (p.has_sg && lane == 0) list[0] = p.E;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const bool in = lane + 64 * i < p.E && lv[i] >= lo;
+      const uint64_t m = __ballot(in);
+      if (in) list[n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
+          lane + 64 * i;
+      n += __popcll(m);
+    }
+    if (WPT > 1 && lane == 0) s_n = n;
   } else {
     // the other waves only re-check: zero the pieces past the row's end
 #pragma unroll
