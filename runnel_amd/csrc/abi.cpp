@@ -216,7 +216,10 @@ Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
   l.fused = off;
   off = align_up(off + sizeof(rmoe::FusedScratch));
   l.logits = off;
-  off = align_up(off + (size_t)T * (E + 1) * sizeof(float));
+  // (as many partial planes as the matrix-core router would use at T, in
+  // both paths, so that the offsets that follow do not depend on the path)
+  const size_t planes = (size_t)rmoe::router_logit_planes(T);
+  off = align_up(off + planes * (size_t)T * (E + 1) * sizeof(float));
   l.idx = off;
   off = align_up(off + (size_t)T * K * sizeof(int32_t));
   l.scores = off;
@@ -237,7 +240,7 @@ Layout layout(int T, int E, int K, int I, int H = 0, bool sorted = false,
     l.hist = off;
     off = align_up(off + (size_t)rmoe::prefill_sort_slices(T, K) * (E + 2) * sizeof(int32_t));
     l.wnorm = off;
-    off = align_up(off + (size_t)E * sizeof(float));
+    off = align_up(off + planes * (size_t)E * sizeof(float));
     if (split) {
       l.split = off;
       off = align_up(off + 2 * (size_t)E * H * sizeof(uint16_t));
@@ -700,6 +703,7 @@ int block_launch(const rmoe_layer* L, const uint16_t* x, int32_t tokens,
   a.idx_out = indices_out;
   a.scores_out = scores_out;
   if (few_eligible(L, tokens, lay.rows != 0)) a.few_bits = L->gate_up.bits;
+  a.logit_planes = lay.rows ? rmoe::router_logit_planes(tokens) : 1;
   if (lay.rows && rmoe::router_mfma_eligible(L->experts, L->hidden))
     e = rmoe::launch_router_mfma(
         a, reinterpret_cast<float*>(static_cast<char*>(ws) + lay.wnorm),

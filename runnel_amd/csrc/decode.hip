@@ -712,14 +712,16 @@ __device__ __forceinline__ void router_logits_body(const DecodeArgs& p, float* w
 #pragma unroll
   for (int cb = 0; cb < C::CBW; ++cb) ss[cb] = 0.f;
   const bool norms = WNORM && blockIdx.x == 0 && wm == 0;
-  const int nst = H / 64;
+  // this workgroup's share of H (blockIdx.z of gridDim.z): stages c0 .. c0 + nst - 1
+  const int nst = H / 64 / (int)gridDim.z;
+  const int c0 = (int)blockIdx.z * nst;
   auto dma = [&](uint16_t* buf, int c) {
 #pragma unroll
     for (int ii = 0; ii < C::ND; ++ii) {
       const int i = wave + C::WAVES * ii;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           8 * i >= BT ? rb : ra, (__attribute__((address_space(3))) void*)(buf + i * 512), 16,
-          src[ii], c * 128, 0, 0);
+          src[ii], (c0 + c) * 128, 0, 0);
     }
   };
 #pragma unroll
@@ -751,8 +753,8 @@ __device__ __forceinline__ void router_logits_body(const DecodeArgs& p, float* w
       float v = ss[cb];
       v += __shfl_xor(v, 16, kWave);
       v += __shfl_xor(v, 32, kWave);
-      if (kg == 0)
-        wnorm[e0 + brow0 - BT + cb * 16 + (lane & 15)] = sqrtf(v) * (1.0f + 1.0f / 1024.0f);
+      // this share's sum of squares (the selection adds the shares)
+      if (kg == 0) wnorm[(size_t)blockIdx.z * p.E + e0 + brow0 - BT + cb * 16 + (lane & 15)] = v;
     }
   }
   // lane (col, kg) of block (mb, cb) holds tokens 4 kg + [0, 4) of expert col
@@ -765,7 +767,7 @@ __device__ __forceinline__ void router_logits_body(const DecodeArgs& p, float* w
       for (int i = 0; i < 4; ++i) {
         const int t = t0 + arow0 + mb * 16 + 4 * kg + i;
         if (t < p.T) {
-          float* o = p.logits + (size_t)t * (p.E + 1) + e;
+          float* o = p.logits + ((size_t)blockIdx.z * p.T + t) * (p.E + 1) + e;
           *o = ACC ? *o + acc[mb][cb][i] : acc[mb][cb][i];
         }
       }
@@ -927,12 +929,28 @@ void router_select_kernel(const DecodeArgs p, const float* wnorm) {
   if (lead) {
     // logits and row bounds: unconditional loads (lanes past E read expert
     // E - 1), so that all of them are in flight together
+    // (the matrix-core logits as partial planes, added in plane order; for a
+    // bf16 gate the row bounds as planes of partial sums of squares)
+    const int NP = max(p.logit_planes, 1);
+    const size_t plane = (size_t)p.T * (p.E + 1);
     float lraw[P], wraw[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
       const int e = min(lane + 64 * i, p.E - 1);
       lraw[i] = lg[e];
       wraw[i] = wnorm[e];
+    }
+    for (int z = 1; z < NP; ++z) {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int e = min(lane + 64 * i, p.E - 1);
+        lraw[i] += lg[z * plane + e];
+        if constexpr (!RQ) wraw[i] += wnorm[(size_t)z * p.E + e];
+      }
+    }
+    if constexpr (!RQ) {
+#pragma unroll
+      for (int i = 0; i < P; ++i) wraw[i] = sqrtf(wraw[i]) * (1.0f + 1.0f / 1024.0f);
     }
     issue_fence();  // keeps these loads from being sunk into per-lane branches
     float lv[P], wn = 0.0f, amax = 0.0f;
@@ -1631,12 +1649,23 @@ static void select_launch(const DecodeArgs& a, const void* wnorm, hipStream_t s)
 
 template <bool ACC, bool WNORM>
 static void launch_logits(const DecodeArgs& a, float* wnorm, hipStream_t s) {
+  const unsigned z = (unsigned)max(a.logit_planes, 1);
   if (a.T >= 4096)
     hipLaunchKernelGGL((router_logits_kernel<64, 64, 2, 2, 3, ACC, WNORM>),
-                       dim3((a.T + 63) / 64, a.E / 64), dim3(256), 0, s, a, wnorm);
+                       dim3((a.T + 63) / 64, a.E / 64, z), dim3(256), 0, s, a, wnorm);
   else
     hipLaunchKernelGGL((router_logits_kernel<32, 32, 2, 2, 4, ACC, WNORM>),
-                       dim3((a.T + 31) / 32, a.E / 32), dim3(256), 0, s, a, wnorm);
+                       dim3((a.T + 31) / 32, a.E / 32, z), dim3(256), 0, s, a, wnorm);
+}
+
+// Shares of H over which the logits kernel splits each tile (each share
+// its own partial plane): a few hundred tokens leave most CUs idle with one
+// workgroup per tile, and the shorter chain of stages ends sooner (512
+// tokens: 245 -> 241 us per block call); from 4096 tokens on the 64 x 64
+// tiles fill the device and the extra planes' traffic cost more (8192
+// tokens: +8 us with two).
+int router_logit_planes(int T) {
+  return T <= 1024 ? 4 : T < 4096 ? 2 : 1;
 }
 
 hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split,

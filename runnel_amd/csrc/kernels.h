@@ -50,6 +50,10 @@ struct DecodeArgs {
   int32_t* idx_out;
   float* scores_out;
   FusedScratch* fs;  // epoch and status words (the few-token router's tagged hand-over)
+  // matrix-core router: its logits come in logit_planes partial planes of
+  // [T, E + 1] (one per share of H, summed in plane order), and for a bf16
+  // gate the row bounds as that many planes of partial sums of squares
+  int logit_planes;
 };
 
 struct QmvArgs {
@@ -132,6 +136,7 @@ hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, int T, int H, fl
                           uint16_t* out, hipStream_t s);
 // Many-token router on the matrix cores with exact selection (prefill).
 bool router_mfma_eligible(int E, int H);
+int router_logit_planes(int T);
 // wnorm: [E] floats; split: [2, E, H] bf16 (quantized gates only)
 hipError_t launch_router_mfma(const DecodeArgs& a, float* wnorm, uint16_t* split,
                               hipStream_t s);
