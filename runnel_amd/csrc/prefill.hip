@@ -289,10 +289,28 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
     }
   }
 
-  // per-wave counts of this wave's run (two chunks of 64 rows per step)
+  // per-wave counts of this wave's run (two chunks of 64 rows per step);
+  // the buckets of the first kKeep steps stay in registers for the ranking
+  // below (no second round trip for them)
+  constexpr int kKeep = 4;
+  int kept[2 * kKeep];
   int* my = s_hist + wave * NB;
   __syncthreads();  // the zeroed counts
-  for (int c0 = q0; c0 < q1; c0 += 128) {
+#pragma unroll
+  for (int k = 0; k < kKeep; ++k) {
+    const int c0 = q0 + 128 * k;
+    kept[2 * k] = kept[2 * k + 1] = 0;
+    if (c0 < q1) {
+      const int ra = c0 + lane, rb = c0 + 64 + lane;
+      const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
+      issue_fence();
+      kept[2 * k] = ea;
+      kept[2 * k + 1] = eb;
+      if (ra < q1) atomicAdd(&my[ea], 1);
+      if (rb < q1) atomicAdd(&my[eb], 1);
+    }
+  }
+  for (int c0 = q0 + 128 * kKeep; c0 < q1; c0 += 128) {
     const int ra = c0 + lane, rb = c0 + 64 + lane;
     const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
     issue_fence();
@@ -416,7 +434,16 @@ __global__ __launch_bounds__(kSortThreads) void prefill_place_kernel(const Prefi
     if (v && (mask >> lane) == 1ull) my[e] += __popcll(mask);
     __builtin_amdgcn_wave_barrier();
   };
-  for (int c0 = q0; c0 < q1; c0 += 128) {
+#pragma unroll
+  for (int k = 0; k < kKeep; ++k) {
+    const int c0 = q0 + 128 * k;
+    if (c0 < q1) {
+      const int ra = c0 + lane, rb = c0 + 64 + lane;
+      rank_chunk(ra, ra < q1 ? kept[2 * k] : 0, ra < q1);
+      if (c0 + 64 < q1) rank_chunk(rb, rb < q1 ? kept[2 * k + 1] : 0, rb < q1);
+    }
+  }
+  for (int c0 = q0 + 128 * kKeep; c0 < q1; c0 += 128) {
     const int ra = c0 + lane, rb = c0 + 64 + lane;
     const int ea = bucket_of(p, min(ra, q1 - 1)), eb = bucket_of(p, min(rb, q1 - 1));
     issue_fence();
