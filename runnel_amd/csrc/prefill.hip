@@ -105,12 +105,14 @@ __device__ __forceinline__ uint32_t word4(const u32x4& v, int i) {
 }
 
 // The bf16 MFMA fragment j (8 consecutive k) of a lane's weight slice (LPC
-// 16-byte loads).
-// OPAQUE (4 bits): keep the nibble-split words opaque to the optimiser,
-// which otherwise turns each code into a bit-field extract plus a
-// conversion instead of one byte conversion; it holds both words live, so
-// only the 128-row tiles (registers to spare) use it.
-template <int BITS, int LPC, bool OPAQUE>
+// 16-byte loads): bf16(fl32(q s + b)).
+// 4 bits: the codes, split into bytes, go through the fp8 (OCP e4m3)
+// conversion: a byte 0..15 is e4m3 q 2^-9 (codes 0-7 subnormal, 8-15 with
+// exponent 1), so scaled by 2^9 it is q exactly, two codes per instruction
+// instead of one byte conversion each (checked for every code and byte
+// position on the device; dense 65536 x 1024 x 2048 4-bit GEMM 283 -> 272
+// us).
+template <int BITS, int LPC>
 __device__ __forceinline__ bf16x8_t dequant_frag(const uint4 (&w)[LPC], int j, float s,
                                                  float b) {
   u32x4 d;
@@ -123,15 +125,16 @@ __device__ __forceinline__ bf16x8_t dequant_frag(const uint4 (&w)[LPC], int j, f
     d.w = pack_bf16x2(fmaf((float)((w1 >> 16) & 0xFFu), s, b), fmaf((float)(w1 >> 24), s, b));
   } else {
     const uint32_t wj = word_of(w[j >> 2], j & 3);
-    uint32_t lo = wj & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
-    uint32_t hi = (wj >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
-    if constexpr (OPAQUE) asm volatile("" : "+v"(lo), "+v"(hi));
-    d.x = pack_bf16x2(fmaf((float)(lo & 0xFFu), s, b), fmaf((float)(hi & 0xFFu), s, b));
-    d.y = pack_bf16x2(fmaf((float)((lo >> 8) & 0xFFu), s, b),
-                      fmaf((float)((hi >> 8) & 0xFFu), s, b));
-    d.z = pack_bf16x2(fmaf((float)((lo >> 16) & 0xFFu), s, b),
-                      fmaf((float)((hi >> 16) & 0xFFu), s, b));
-    d.w = pack_bf16x2(fmaf((float)(lo >> 24), s, b), fmaf((float)(hi >> 24), s, b));
+    const uint32_t lo = wj & 0x0F0F0F0Fu;         // codes 0, 2, 4, 6
+    const uint32_t hi = (wj >> 4) & 0x0F0F0F0Fu;  // codes 1, 3, 5, 7
+    const f32x2_t l0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, false);
+    const f32x2_t l1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, true);
+    const f32x2_t h0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, false);
+    const f32x2_t h1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, true);
+    d.x = pack_bf16x2(fmaf(l0.x, s, b), fmaf(h0.x, s, b));
+    d.y = pack_bf16x2(fmaf(l0.y, s, b), fmaf(h0.y, s, b));
+    d.z = pack_bf16x2(fmaf(l1.x, s, b), fmaf(h1.x, s, b));
+    d.w = pack_bf16x2(fmaf(l1.y, s, b), fmaf(h1.y, s, b));
   }
   return __builtin_bit_cast(bf16x8_t, d);
 }
@@ -685,7 +688,7 @@ struct Gemm {
     bf16x8_t a[MBA], bf[QPW];
     read_a(0, a);
 #pragma unroll
-    for (int qq = 0; qq < QPW; ++qq) bf[qq] = dequant_frag<BITS, C::LPC, (BM >= 64)>(w[qq], 0, s[qq], b[qq]);
+    for (int qq = 0; qq < QPW; ++qq) bf[qq] = dequant_frag<BITS, C::LPC>(w[qq], 0, s[qq], b[qq]);
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
       bf16x8_t na[MBA], nbf[QPW];
@@ -693,7 +696,7 @@ struct Gemm {
         read_a(j + 1, na);
 #pragma unroll
         for (int qq = 0; qq < QPW; ++qq)
-          nbf[qq] = dequant_frag<BITS, C::LPC, (BM >= 64)>(w[qq], j + 1, s[qq], b[qq]);
+          nbf[qq] = dequant_frag<BITS, C::LPC>(w[qq], j + 1, s[qq], b[qq]);
       }
 #pragma unroll
       for (int mb = 0; mb < MBA; ++mb)
@@ -864,6 +867,10 @@ struct Wide {
   // which touched 16 rows: the memory pipeline, not the bytes, was the cost.
   static constexpr int PS = 8 * 64 / KB * SB;  // stages per block (8 groups)
   static constexpr int NSB = 2;                // block load instructions
+  // A fragments read ahead of their MFMAs (dense 65536 x 1024 x 2048 4-bit
+  // GEMM: each pair read just before its MFMAs 276 us, 2 ahead 255-260, 3
+  // ahead 254-261, 4 ahead 261-326)
+  static constexpr int PF = 2;
 
   struct Bw {
     u32x4 w[QPW];
@@ -1034,19 +1041,35 @@ struct Wide {
     }
     if constexpr (H == 0) scales<POS / SB>(bs, bb, sc, bi);
     const uint16_t* cb = bufs[BUF];
+    // The first PF A fragments of a step are read before its
+    // dequantisation, then each MFMA group reads the fragment PF ahead, so
+    // no MFMA waits for a read just issued.
+    constexpr int NPF = MBA < PF ? MBA : PF;
+    auto read_a = [&](int j, int mb) {
+      return __builtin_bit_cast(bf16x8_t,
+                                *reinterpret_cast<const u32x4*>(cb + mb * 1024 + rd[j]));
+    };
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      bf16x8_t bf[QPW];
+      bf16x8_t a[MBA], bf[QPW];
+#pragma unroll
+      for (int mb = 0; mb < NPF; ++mb) a[mb] = read_a(j, mb);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int qq = 0; qq < QPW; ++qq)
-        bf[qq] = dequant_frag<BITS, 1, true>(
+        bf[qq] = dequant_frag<BITS, 1>(
             *reinterpret_cast<const uint4(*)[1]>(&cur.w[qq]), 2 * H + j, sc[qq], bi[qq]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int mb = 0; mb < MBA; ++mb) {
-        const bf16x8_t a =
-            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4*>(cb + mb * 1024 + rd[j]));
+        if (mb + NPF < MBA) a[mb + NPF] = read_a(j, mb + NPF);
 #pragma unroll
-        for (int qq = 0; qq < QPW; ++qq) acc[mb][qq] = mfma(a, bf[qq], acc[mb][qq]);
+        for (int qq = 0; qq < QPW; ++qq) acc[mb][qq] = mfma(a[mb], bf[qq], acc[mb][qq]);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MBA; ++mb) {
+        if (mb + NPF < MBA) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, QPW, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
