@@ -31,13 +31,15 @@
 //   S  waves 6 and 7: one shared pair each; its activation is published
 //      device-wide after the routed loads are out
 //   K  wave 0 ranks the XCD's logits: 4 keys per lane sorted locally, then
-//      top_k rounds of a DPP wave maximum
+//      rounds of a DPP wave maximum up to this XCD's slot (the rest of the
+//      top_k rounds once the routed loads are out)
 //   G  this XCD's routed expert: two pairs per wave and, right behind
 //      their rows, eight down rows per wave are loaded; activations to the
 //      XCD's L2
-//   D  the routed rows' dots, and two shared rows per loader wave; the
-//      results go to LDS and one wave stores them after the layer's last
-//      barrier
+//   D  the routed rows' dots, and (8-bit) two shared rows per loader wave;
+//      4-bit layers reduce the shared rows on wave 1 before D, while the
+//      routed activations are on their way.  The results go to LDS and one
+//      wave stores them after the layer's last barrier
 //   O  (after the last layer) every workgroup combines 8 output rows
 //
 // Values handed between workgroups are tagged words, (bf16 value << 16) |
@@ -72,6 +74,7 @@ namespace {
 constexpr int kThreads = kFusedThreads;
 constexpr int kWaves = kThreads / 64;
 constexpr int kPollWave = 0;  // ranks the logits and computes the scores
+constexpr int kShDownWave = 1;  // 4-bit: the workgroup's shared down rows
 
 // XCD-local hand-over (between workgroups on one XCD): stores reach the
 // XCD's L2 (the vector L1 writes through); loads with sc0 nt skip the L1
@@ -592,6 +595,24 @@ __device__ __forceinline__ void gate_row_from_lds(GateRow<RQ>& r, const char* sl
   }
 }
 
+// Eight down rows through a buffer resource (rows past `rows` read as zero).
+template <int BITS>
+__device__ __forceinline__ void load_rows_buf(RowsRegs<BITS>& r, const QW& bank, uint32_t rows,
+                                              uint32_t row0, int lane) {
+  constexpr int I = kFusedI;
+  constexpr int WPR = I * BITS / 32;
+  const __amdgpu_buffer_rsrc_t rp =
+      rsrc(lane < 32 ? (const void*)bank.s : (const void*)bank.b, rows * (I / 64) * 2);
+  r.pw = __builtin_amdgcn_raw_buffer_load_b32(rp, row0 * (I / 64) * 2 + (lane & 31) * 4, 0, 0);
+  const __amdgpu_buffer_rsrc_t rw = rsrc(bank.w, rows * WPR * 4);
+#pragma unroll
+  for (int i = 0; i < RowsRegs<BITS>::N; ++i) {
+    const u32x4 v =
+        __builtin_amdgcn_raw_buffer_load_b128(rw, (row0 * WPR + (i * 64 + lane) * 4) * 4, 0, kNt);
+    r.w[i] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+}
+
 // Gate/up pair (up row c, gate row c + I of bank row base) through buffer
 // loads: the same registers and lane layout as load_pair_params/words.
 template <int BITS, int CPL>
@@ -672,10 +693,12 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   const int row = j + kXcdWgs * wave;     // router row of this wave (< 256)
   const int vg = j + kXcdWgs * wave;      // routed pairs vg, vg + 256
   const int rrow0 = (j * kWaves + wave) * kXcdRows;  // routed down rows (8)
-  // shared: pair of waves 6 and 7, down rows 2 q, 2 q + 1 of the workgroup's 8
+  // shared: pair of waves 6 and 7; the workgroup's eight down rows hsr0 ..
+  // hsr0 + 7 (8-bit: rows 2 q, 2 q + 1 of them on loader q; 4-bit: all on
+  // wave kShDownWave)
   const bool sp_wave = wave >= kSharedPairWave;
   const int spair = xcd * kSharedPairsPerXcd + (j + kXcdWgs * (wave - kSharedPairWave));
-  const int hs0 = xcd * kXcdWaves + j * kXcdRows + 2 * q;
+  const int hsr0 = xcd * kXcdWaves + j * kXcdRows;
   const int c_own = j * (kWaves * kXcdRows) + wave * kCombRows;  // combine rows (pollers)
   FusedScratch* sc = p.scratch;
 
@@ -703,8 +726,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
   PairRegs<CPL> pr[kRoutedPairs];
   PairRegs<CPL> spr;
   RowsRegs<BITS> dr;
+  RowsRegs<BITS> shr;
   DownRegs<S::DN_WPL> sdr[2];
   uint32_t sdpw[2] = {0, 0};
+  const int hs0 = hsr0 + 2 * q;
   LoaderRegs ld;
 
   // Loader waves: every routing-independent load of layer L (unconditional,
@@ -730,9 +755,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         }
       }
     }
+    if constexpr (BITS == 8) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      load_down_row_buf<BITS>(sdr[t], sdpw[t], L.sdn, has_shared ? H : 0, hs0 + t, lane);
+      for (int t = 0; t < 2; ++t)
+        load_down_row_buf<BITS>(sdr[t], sdpw[t], L.sdn, has_shared ? H : 0, hs0 + t, lane);
+    }
     if (q >= 2)
       load_pair_buf<BITS, CPL>(spr, L.sgu, sp_wave && has_shared ? 2 * I : 0,
                                sp_wave ? spair : 0, lane);
@@ -871,6 +898,8 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     float lv[kPer];
     float m_top = 0.0f;
     uint32_t my = 0;
+    uint32_t k[kPer] = {0u, 0u, 0u, 0u};
+    uint32_t sel[NU - 1];
     if (wave == kPollWave) {
       const __amdgpu_buffer_rsrc_t rs = rsrc(sc->logits[xcd], E * 4);
       uint32_t w[kPer] = {0u, 0u, 0u, 0u};
@@ -887,7 +916,6 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         if (give_up(wst, spin)) break;
         __builtin_amdgcn_s_sleep(1);
       }
-      uint32_t k[kPer];
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
         const int e = 4 * lane + i;
@@ -900,11 +928,10 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       cswap_desc(k[0], k[2]);
       cswap_desc(k[1], k[3]);
       cswap_desc(k[1], k[2]);
-      uint32_t sel[NU - 1];
 #pragma unroll
       for (int jj = 0; jj < NU - 1; ++jj) {
         sel[jj] = 0;
-        if (jj < K) {
+        if (jj < K && jj <= xcd) {
           const uint32_t best = wave_max_u32(k[0]);
           sel[jj] = best;
           if (k[0] == best) {
@@ -916,10 +943,11 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         }
       }
       m_top = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
+      uint32_t mine = 0;
 #pragma unroll
       for (int jj = 0; jj < NU - 1; ++jj)
-        if (lane == jj) my = sel[jj];
-      if (lane < K) s_idx[lane] = (int)(0xFFFFu - (my & 0xFFFFu));
+        if (jj == xcd) mine = sel[jj];
+      if (routed && lane == 0) s_idx[xcd] = (int)(0xFFFFu - (mine & 0xFFFFu));
     }
     __syncthreads();
 
@@ -941,6 +969,32 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
       // memory-side cache)
       load_rows_words<BITS>(dr, L.dn, e * H + (size_t)rrow0, lane);
       issue_fence();
+    }
+    if (BITS == 4 && wave == kShDownWave) {
+      // the shared down rows behind this wave's routed rows
+      load_rows_buf<BITS>(shr, L.sdn, has_shared ? H : 0, hsr0, lane);
+      issue_fence();
+    }
+    if (wave == kPollWave) {
+      // the ranking rounds past this XCD's slot, now that the routed loads
+      // are out (the K barrier waited only for the rounds up to it: 4-bit
+      // chain 11.12 -> 11.03 us per layer, 8-bit 12.31 -> 12.27)
+#pragma unroll
+      for (int jj = 0; jj < NU - 1; ++jj) {
+        if (jj < K && jj > xcd) {
+          const uint32_t best = wave_max_u32(k[0]);
+          sel[jj] = best;
+          if (k[0] == best) {
+            k[0] = k[1];
+            k[1] = k[2];
+            k[2] = k[3];
+            k[3] = 0;
+          }
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < NU - 1; ++jj)
+        if (lane == jj) my = sel[jj];
     }
     if (sp_wave && lane == 0) store_coherent_u32(sc->sact[cur] + spair, tagged(s_a, tag));
     if (routed) {
@@ -997,15 +1051,33 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
         s_coef[K] = sg_row ? round_bf16(sigmoid(bf16_to_f32(wsg >> 16))) : 1.0f;
     }
 
-    // ---- collect the activations: routed (XCD-local) and shared.
+    // ---- the shared activations.  4-bit: wave kShDownWave collects them
+    // and reduces the workgroup's eight shared down rows while the routed
+    // activations are on their way (40-layer chain 11.42 -> 11.12 us per
+    // layer; the same at 8 bits measured 12.3 -> 15.2 us, so 8-bit layers
+    // keep two shared rows on each loader wave in D).
+    if (BITS == 8 && (wave == 4 || wave == 5))
+      poll_tagged<1, kSc1>(sc->sact[cur], I, tag, s_ash, lane, wave - 4, wst);
+    if (BITS == 4 && wave == kShDownWave) {
+      poll_tagged<2, kSc1>(sc->sact[cur], I, tag, s_ash, lane, 0, wst);
+      float ysh[NR];
+      rows_dot<BITS>(shr, s_ash, lane, ysh);
+      constexpr int kLanesPerRow = BITS == 8 ? 32 : 16;
+      if ((lane & (kLanesPerRow - 1)) == 0) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+          s_yo[kWaves * kXcdRows + i * (64 / kLanesPerRow) + lane / kLanesPerRow] =
+              tagged(has_shared ? f32_to_bf16(ysh[i]) : 0u, tag);
+      }
+    }
+
+    // ---- collect the routed activations (XCD-local).
     if (routed && (wave == 2 || wave == 3))
       poll_tagged<1, kXcdLoadAux>(sc->xact[xcd], I, tag, s_act, lane, wave - 2, wst);
-    if (wave == 4 || wave == 5)
-      poll_tagged<1, kSc1>(sc->sact[cur], I, tag, s_ash, lane, wave - 4, wst);
     __syncthreads();
 
-    // ---- D: eight routed down rows per wave, two shared rows per loader
-    // wave; results to LDS.
+    // ---- D: eight routed down rows per wave (8-bit: two shared rows per
+    // loader wave as well); results to LDS.
     if (routed) {
       float y[NR];
       rows_dot<BITS>(dr, s_act, lane, y);
@@ -1019,7 +1091,7 @@ __global__ __launch_bounds__(kThreads) void fused_decode_kernel(const FusedArgs 
     } else if (lane < kXcdRows) {
       s_yo[wave * kXcdRows + lane] = tagged(0u, tag);
     }
-    if (loader) {
+    if (BITS == 8 && loader) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const float y = has_shared ? row_dot<BITS>(sdr[t], sdpw[t], s_ash, lane) : 0.0f;
