@@ -125,6 +125,36 @@ def test_block_prefill_512_tokens_8bit(torch_cuda):
     assert cosine(got.reshape(-1), mx_.reshape(-1)) >= MIN_COS
 
 
+@pytest.mark.parametrize("bits", [8, 4])
+def test_prefill_512_tokens_deterministic(torch_cuda, bits):
+    """The 512-token chunk through a full-size layer: two calls give the same
+    bits (no result depends on which workgroup finishes first), and the
+    4-bit layer meets the contract like the 8-bit one above."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lw = synthetic.make_layer(5150 + bits, bits=bits)
+    h = lw.handle()
+    x = synthetic.make_x(13, 512, 2048)
+    out1 = native.moe_block(h, x)
+    out2 = native.moe_block(h, x)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    if bits == 4:
+        out, idx, _ = native.moe_block(h, x, return_routing=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out1)
+        L = layer_from_dev(lw)
+        xb = host_bf16(x)
+        ref, ref_idx, _ = M.block_forward(L, xb, mode="prefill")
+        assert np.array_equal(idx.cpu().numpy(), ref_idx)
+        got = M.bf16_to_f32(host_bf16(out))
+        assert _mismatches(got, M.bf16_to_f32(ref)) <= got.size // 500
+        mlx, _, _ = M.block_forward(L, xb, mode="mlx")
+        mx_ = M.bf16_to_f32(mlx)
+        assert np.abs(got - mx_).max() <= MAX_ABS
+        assert cosine(got.reshape(-1), mx_.reshape(-1)) >= MIN_COS
+
+
 @pytest.mark.parametrize("shape", [dict(hidden=1024, experts=128, top_k=8),
                                    dict(hidden=512, experts=64, top_k=6),
                                    # the widest eligible rows: two passes of
