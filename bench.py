@@ -246,6 +246,61 @@ def run_decode_chain(args, torch):
     }
 
 
+def run_eager_module(torch, lw, calls=400, warmup=50):
+    """The drop-in surface called eagerly, as mlx-lm calls it: an unfused
+    ``SparseMoeBlock`` holding one 8-bit layer (stock SwitchGLU with separate
+    gate / up banks, shared expert and gates), installed with
+    ``fuse_routed_gate_up`` and then called as ``layer.mlp(x)`` on one token
+    ([1, 1, 2048]) `calls` times back to back, every call eager from Python
+    (argument checks, output allocation, the C call, a plain launch).  HIP
+    events around the calls; the figure includes the host's per-call time
+    whenever the host is slower than the kernel."""
+    from types import SimpleNamespace
+    from runnel_amd import SparseMoeBlock, fuse_routed_gate_up
+    H, I, E = 2048, 512, 256
+    blk = SparseMoeBlock(H, I, E, 8, shared_expert_intermediate_size=I, bits=8, device="cuda")
+    with torch.no_grad():
+        blk.gate.weight.copy_(lw.router_w)
+        w, sc, b = lw.gate_up
+        sm = blk.switch_mlp
+        for mod, lo in ((sm.up_proj, 0), (sm.gate_proj, I)):
+            mod.weight.copy_(w[:, lo:lo + I])
+            mod.scales.copy_(sc[:, lo:lo + I])
+            mod.biases.copy_(b[:, lo:lo + I])
+        for t, src in zip((sm.down_proj.weight, sm.down_proj.scales, sm.down_proj.biases), lw.down):
+            t.copy_(src)
+        w, sc, b = (t.reshape(2 * I, -1) for t in lw.shared_gate_up)
+        se = blk.shared_expert
+        for mod, lo in ((se.up_proj, 0), (se.gate_proj, I)):
+            mod.weight.copy_(w[lo:lo + I])
+            mod.scales.copy_(sc[lo:lo + I])
+            mod.biases.copy_(b[lo:lo + I])
+        for t, src in zip((se.down_proj.weight, se.down_proj.scales, se.down_proj.biases),
+                          lw.shared_down):
+            t.copy_(src.reshape(t.shape))
+        blk.shared_expert_gate.weight.copy_(lw.shared_gate_w.reshape(1, H))
+    model = SimpleNamespace(language_model=SimpleNamespace(layers=[SimpleNamespace(mlp=blk)]))
+    installed = fuse_routed_gate_up(model)
+    x = torch.randn(1, 1, H, device="cuda").to(torch.bfloat16)
+    with torch.no_grad():
+        for _ in range(warmup):
+            y = blk(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(calls):
+            y = blk(x)
+        e1.record()
+        torch.cuda.synchronize()
+    blk.check_status()
+    us = e0.elapsed_time(e1) * 1000.0 / calls
+    del blk, model, y
+    return {"workload": "SparseMoeBlock(x) on one token, eager, after fuse_routed_gate_up (one "
+                        "8-bit layer: hidden 2048, 256 experts, top-8 + shared, inter 512)",
+            "us_per_call": round(us, 2), "calls": calls, "installed_layers": installed,
+            "launch": "eager plain launches"}
+
+
 def run_decode_single(torch, bits, copies=16, calls=64, reps=20, warmup=3, seed0=1000):
     """One MoE layer per call at batch-1 decode (rmoe_moe_block, one token:
     the single-launch kernel with one layer), the single-layer workloads of
@@ -560,6 +615,8 @@ def main():
         # one layer per call at 8 and 4 bits, rotating over 16 copies
         out["decode_1layer_8bit"] = run_decode_single(torch, 8)
         out["decode_1layer_4bit"] = run_decode_single(torch, 4)
+        # the module surface called eagerly (layer.mlp(x) on one token)
+        out["eager_module_1token"] = run_eager_module(torch, res["stack"][0])
     if not args.no_prefill:
         # prefill figures of the same build (one layer per call, HIP events)
         # enough warm-up calls for the clocks to settle: three back-to-back
