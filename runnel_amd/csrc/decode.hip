@@ -295,7 +295,10 @@ __device__ __forceinline__ void bf16_gate_partials(const uint16_t* wr, const uin
     for (int i = 0; i < kRouterBatch; ++i) {
       const int c = c0 + 64 * i;
       wv[i] = make_uint4(0, 0, 0, 0);
-      if (c < chunks) wv[i] = load16_stream(wr + c * 8);
+      // (the default cache policy: a layer's router rows are read every
+      // call, and the memory-side cache keeps some of them between calls;
+      // 4 tokens through the 40-layer stack 28.45 -> 28.22 us per layer call)
+      if (c < chunks) wv[i] = load16(wr + c * 8);
 #pragma unroll
       for (int k = 0; k < TB; ++k) {
         xv[k][i] = make_uint4(0, 0, 0, 0);
@@ -355,7 +358,7 @@ __device__ __forceinline__ void q8_gate_partials(const QW& bank, size_t row, con
       wv[i] = make_uint4(0, 0, 0, 0);
       sv[i] = bv[i] = 0;
       if (c < chunks) {
-        wv[i] = load16_stream(wr + c * 4);
+        wv[i] = load16(wr + c * 4);  // (default cache policy, as above)
         sv[i] = sr[c >> 2];
         bv[i] = br[c >> 2];
       }
