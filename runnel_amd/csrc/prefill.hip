@@ -1241,36 +1241,49 @@ __attribute__((amdgpu_waves_per_eu(Engine<BITS, BM, MODE>::MIN_WAVES))) void pre
 // ---------------------------------------------------------------- combine
 // out[t] = bf16(sum_j score_j y[t K + j] + sg_t y[T K + t]) (+ residual):
 // the slots in order, then the shared expert, as the decode kernels sum.
+// From this many tokens the combine requests all of a token's rows at once
+// (8192 tokens: 67.1 -> 56.7 us per call, 5.9 TB/s); below it one row per
+// round trip was faster (512 tokens: 5.9 against 6.5 us).
+constexpr int kCombineBatchTokens = 2048;
+
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const PrefillArgs p) {
   const int t = blockIdx.x;
   const int H = p.H;
   const int K = p.K;
   const int units = K + p.has_shared;
   const float* sc = p.scores + (size_t)t * p.score_stride;
+  auto row_of = [&](int u) { return u < K ? (size_t)t * K + u : (size_t)p.T * K + t; };
+  auto add_row = [](float (&acc)[8], const uint4 v, float w) {
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] += w * bf16_lo(vv[i]);
+      acc[2 * i + 1] += w * bf16_hi(vv[i]);
+    }
+  };
   for (int h0 = threadIdx.x * 8; h0 < H; h0 += 256 * 8) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int u = 0; u < units; ++u) {
-      const size_t row = u < K ? (size_t)t * K + u : (size_t)p.T * K + t;
-      const uint4 v = load16(p.y + row * H + h0);
-      const float w = sc[u];
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    uint4 r = make_uint4(0u, 0u, 0u, 0u);
+    if (units <= kMaxFusedUnits && p.T >= kCombineBatchTokens) {
+      // every unit's row (and the residual) requested at once, then summed
+      // in slot order: one load in flight per unit instead of one per
+      // round trip
+      uint4 v[kMaxFusedUnits];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += w * bf16_lo(vv[i]);
-        acc[2 * i + 1] += w * bf16_hi(vv[i]);
-      }
+      for (int u = 0; u < kMaxFusedUnits; ++u)
+        if (u < units) v[u] = load16_stream(p.y + row_of(u) * H + h0);
+      if (p.residual) r = load16(p.residual + (size_t)t * H + h0);
+#pragma unroll
+      for (int u = 0; u < kMaxFusedUnits; ++u)
+        if (u < units) add_row(acc, v[u], sc[u]);
+    } else {
+      for (int u = 0; u < units; ++u) add_row(acc, load16(p.y + row_of(u) * H + h0), sc[u]);
+      if (p.residual) r = load16(p.residual + (size_t)t * H + h0);
     }
     uint32_t o[4];
-    uint32_t rr[4] = {0, 0, 0, 0};
-    if (p.residual) {
-      const uint4 r = load16(p.residual + (size_t)t * H + h0);
-      rr[0] = r.x;
-      rr[1] = r.y;
-      rr[2] = r.z;
-      rr[3] = r.w;
-    }
+    const uint32_t rr[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float a = round_bf16(acc[2 * i]);
