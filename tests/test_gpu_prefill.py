@@ -155,6 +155,40 @@ def test_prefill_512_tokens_deterministic(torch_cuda, bits):
         assert cosine(got.reshape(-1), mx_.reshape(-1)) >= MIN_COS
 
 
+def test_long_prefill_combine_bit_exact(torch_cuda):
+    """2048 tokens through a full-size layer (128-row tiles; the combine
+    requests all of a token's rows at once): the output equals, bit for bit,
+    the combine restated on the host (fp32 fma over the slots in order, bf16
+    rounding, then the residual) from the same routing's per-slot rows (the
+    uncombined call); a second call with other inputs on the same workspace
+    as well, so no row of an earlier call is read in place of the current
+    one."""
+    torch = torch_cuda
+    from runnel_amd import native, synthetic
+    lw = synthetic.make_layer(5160, bits=8)
+    gu = native.qweight_struct(*lw.gate_up, 8)
+    dn = native.qweight_struct(*lw.down, 8)
+    T, K, H, E = 2048, 8, 2048, 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5161)
+    for rep in range(2):
+        x = synthetic.make_x(5162 + rep, T, H)
+        res = synthetic.make_x(5170 + rep, T, H)
+        idx = torch.rand(T, E, generator=g, device="cuda").argsort(dim=1)[:, :K].contiguous()
+        w = torch.rand(T, K, generator=g, device="cuda")
+        out = native.switch_combine(x, idx, w, gu, dn, residual=res)
+        y = native.switch_glu(x, idx, gu, dn)
+        torch.cuda.synchronize()
+        yf = M.bf16_to_f32(host_bf16(y))
+        wf = w.cpu().numpy()
+        acc = np.zeros((T, H), np.float32)
+        for j in range(K):
+            acc = M.fma32(wf[:, j:j + 1], yf[:, j, :], acc)
+        ref = M.round_bf16(M.bf16_to_f32(host_bf16(res)) + M.round_bf16(acc))
+        got = M.bf16_to_f32(host_bf16(out))
+        assert np.array_equal(got, ref), f"call {rep}: {int((got != ref).sum())} values differ"
+
+
 @pytest.mark.parametrize("shape", [dict(hidden=1024, experts=128, top_k=8),
                                    dict(hidden=512, experts=64, top_k=6),
                                    # the widest eligible rows: two passes of
