@@ -112,7 +112,7 @@ def calibrate_copy(torch, gib: int = 1, reps: int = 5):
 
 
 def measured_read_gbps(torch, gib: int = 4, reps: int = 10):
-    """The box's achievable HBM read bandwidth: rmoe_stream_read (16-byte
+    """The GPU's achievable HBM read bandwidth: rmoe_stream_read (16-byte
     loads, every byte once) over a buffer far larger than the 256 MB MALL,
     best launch shape of a small sweep, HIP events on the current stream."""
     from runnel_amd import native
@@ -511,7 +511,7 @@ def main():
                     help="run only the plain copy kernel used to scale HBM counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path "
+        print(f"bench.py runs on one GPU: the library has no multi-GPU path "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         return 2
 

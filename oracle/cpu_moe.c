@@ -28,7 +28,7 @@
  *    baseline ("port") and a second, independent implementation of the same
  *    contract as oracle/moe_ref.py.  The semantics follow the mlx-lm
  *    SparseMoeBlock that calls src/runnel/mlx.py:57-82; the bf16 rounding
- *    points and the top-k tie rule are this build's own definition, because
+ *    points and the top-k tie rule are this library's own definition, because
  *    mlx/mlx-lm are third-party code that is not available here.
  *
  * Build: oracle/Makefile (gcc -O2 -fopenmp -ffp-contract=off).

@@ -25,7 +25,7 @@ What it restates, and where from:
   src/runnel/mlx.py:59-63,80-81 (mlx-lm): stable sort of the flattened
   (token, slot) expert ids.
 
-Definitions that are this build's own (mlx / mlx-lm cannot run here, so the
+Definitions that are this library's own (mlx / mlx-lm cannot run here, so the
 exact bf16 rounding points inside ``gather_qmm`` and the tie order of
 ``argpartition`` are unpinned):
 
@@ -45,14 +45,14 @@ exact bf16 rounding points inside ``gather_qmm`` and the tie order of
   against the float64 dot, and by constructed double-rounding cases for
   ``fma32`` itself (tests/test_oracle.py).  mlx's quantized_matmul order is
   third-party and unpinned; the mlx-lm-style evaluation is held to the
-  north-star tolerance instead.
+  end-to-end tolerance (max-abs <= 2e-2, cosine >= 0.9999) instead.
 * ``block_forward(mode="contract")`` is the HIP kernels' contract: fp32/f64
   arithmetic with bf16 rounding of x_up, x_gate, the SwiGLU activation, each
   expert's down output, the router probabilities, the renormalisation
   denominator (mlx-lm's ``scores.sum(-1)`` of bf16 scores is bf16), the
   scores, the shared gate and the block output.  ``mode="mlx"`` adds the extra bf16 roundings an
   op-by-op mlx-lm evaluation performs (silu output, score products, the
-  routed sum, the gated shared term)
+  routed sum, the gated shared term); the end-to-end tolerance
   (max-abs <= 2e-2, cosine >= 0.9999) is checked against it.
   ``mode="prefill"`` is the contract of the expert-sorted grouped GEMM used
   when a call routes at least 64 (token, slot) rows (the reference's sort
@@ -310,7 +310,7 @@ def rms_norm(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
     (``mx.fast.rms_norm(x, w, eps)``; the checkpoints store the effective
     weight): bf16 bits [T, H] -> bf16 bits [T, H].
 
-    This build's fixed order: s = sum x_k^2 in the router contract's order
+    This library's fixed order: s = sum x_k^2 in the router contract's order
     (8-element chunks, lane l of 64 takes chunks l, l+64, ... from +0, then
     the butterfly; the squares of bf16 values are exact in fp32), then in
     fp32 with correct rounding ms = s / H, v = ms + eps, r = 1 / sqrt(v), and

@@ -6,7 +6,7 @@ Reads the reference's result files (data, not source) under
 next to this script.  Only the fields that pin arithmetic are kept: the
 probe parameters, the CPU-oracle checksum, the first eight oracle outputs,
 and the SHA-256 of the datasets the reference wrote.  Run it in a container
-that has the reference mounted; the GPU box never needs it.
+that has the reference mounted; the GPU tests never need it.
 """
 
 from __future__ import annotations

@@ -395,7 +395,7 @@ def test_kernels_refuse_host_tensors():
         native.quantize(torch.zeros(4, 64), 8)
 
 
-def test_bench_byte_model_matches_the_survey_figures():
+def test_bench_byte_model_matches_the_layer_byte_counts():
     import bench
     assert bench.layer_bytes(2048, 512, 256, 8, 8) == 31_141_888
     assert bench.layer_bytes(2048, 512, 256, 8, 4) == 16_986_112

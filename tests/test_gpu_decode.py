@@ -1,6 +1,6 @@
 """GPU parity of the decode-shaped path against the oracle.
 
-Bar: expert indices bit-exact; outputs within the north-star tolerance
+Bar: expert indices bit-exact; outputs within the end-to-end tolerance (max-abs 2e-2, cosine 0.9999)
 (max-abs <= 2e-2, cosine >= 0.9999 in bf16) of the mlx-lm-style oracle, and
 tightly (a few bf16 ulps) against the kernels' own contract oracle.
 """

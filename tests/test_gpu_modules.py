@@ -63,7 +63,7 @@ def _contract_mismatches(got_bits, ref_bits):
     return int((np.abs(g - r) > tol).sum())
 
 
-def _north_star(got_bits, ref_bits):
+def _maxabs_cosine(got_bits, ref_bits):
     g, r = M.bf16_to_f32(got_bits), M.bf16_to_f32(ref_bits)
     return float(np.abs(g - r).max()), cosine(g, r)
 
@@ -100,7 +100,7 @@ def test_installer_on_a_device_model(torch_cuda, bits):
             assert _contract_mismatches(got, ref) <= got.size // 500, (i, T)
             mlx, _, _ = M.block_forward(L, x, mode="mlx")
             for out in (got, before[i, T]):
-                err, cos = _north_star(out, mlx)
+                err, cos = _maxabs_cosine(out, mlx)
                 assert err <= MAX_ABS and cos >= MIN_COS, (i, T, err, cos)
         blk.check_status()
     torch.cuda.synchronize()

@@ -2,7 +2,7 @@
 (token, slot) rows) against the oracle's prefill contract: every dequantised
 weight rounded to bf16, then the decode contract's rounding points.  Outputs
 are held to a bf16 rounding step of that contract (a few mismatches allowed
-for accumulation order) and to the north-star tolerance of the mlx-lm-style
+for accumulation order) and to the end-to-end tolerance (max-abs 2e-2, cosine 0.9999) of the mlx-lm-style
 evaluation; routing is bit-exact."""
 
 import numpy as np

@@ -3,7 +3,7 @@
 routing bit-exact against the oracle's quantized-gate contract on every path
 that ranks experts (the per-token router, the single-launch decode, the
 chained decode and the matrix-core prefill router), outputs within a bf16
-rounding step of the contract and within the north-star tolerance of the
+rounding step of the contract and within the end-to-end tolerance (max-abs 2e-2, cosine 0.9999) of the
 mlx-lm-style evaluation."""
 
 import numpy as np
